@@ -1,0 +1,148 @@
+/*
+ * wayfinder_hip.h -- C ABI of libwayfinder_hip.so, the MI355X (gfx950) implementation of
+ * Wayfinder's causal top-K address retrieval plus sparse ("meat") attention forward.
+ *
+ * Every entry point replaces one function of the reference's Python kernel layer
+ * (routing_attention/kernels/, pure PyTorch there); the reference file:line each one
+ * stands in for is given beside it. The reference has no FFI of its own: the binding a
+ * maintainer would add on the reference side is a ctypes stub.
+ *
+ * Conventions
+ *  - All tensor arguments are device pointers (hipMalloc'd or from the PyTorch caching
+ *    allocator). Shapes and strides are in ELEMENTS, int64. The library never allocates,
+ *    frees or keeps a pointer after the call returns; the caller owns every buffer,
+ *    including the optional workspace.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream). Work is enqueued
+ *    asynchronously; no entry point synchronises the host.
+ *  - Return value: WF_OK (0) or a wf_status code. The message of the last failure on the
+ *    calling thread is available from wf_last_error(). Argument validation happens before
+ *    any HIP call, so contract errors are reported even on a machine without a GPU.
+ *  - Indices are int32. Index sets are emitted in canonical order: score descending, ties
+ *    to the lower key index, pad slots last. The reference returns an unspecified order
+ *    (torch.topk(sorted=False)); compare as sets.
+ */
+#ifndef WAYFINDER_HIP_H
+#define WAYFINDER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WF_ABI_VERSION 1
+
+typedef enum wf_status {
+    WF_OK = 0,
+    WF_ERR_INVALID_ARGUMENT = 1, /* shape / rank / stride / pointer contract violated  */
+    WF_ERR_UNSUPPORTED = 2,      /* valid request outside what the kernels implement   */
+    WF_ERR_WORKSPACE = 3,        /* workspace missing or smaller than required         */
+    WF_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed         */
+} wf_status;
+
+typedef enum wf_dtype {
+    WF_DTYPE_F32 = 0,
+    WF_DTYPE_F16 = 1,
+    WF_DTYPE_BF16 = 2
+} wf_dtype;
+
+/* Readout flags (wf_sparse_readout_fwd / wf_fused_args.flags). */
+#define WF_FLAG_MASK_PADS 0x1u /* slots s > t of rows t < k_eff-1 (the pad slots written
+                                  by the retrieval) get zero weight. Off = reference
+                                  behaviour: pads are attended (causal_topk.py:37-57). */
+
+/* Library ABI version (WF_ABI_VERSION of the build). No reference counterpart. */
+int wf_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). No reference counterpart. */
+const char* wf_last_error(void);
+
+/* Number of bytes of device workspace wf_causal_topk_fwd needs for this shape
+ * (the per-chunk key magnitude bounds of the screening stage). */
+size_t wf_causal_topk_workspace_bytes(int64_t B, int64_t T, int64_t R, int64_t top_k);
+
+/*
+ * Causal top-K retrieval.
+ * Replaces: causal_topk (routing_attention/kernels/causal_topk.py:470-521) with
+ *           method auto/fused_causal -> _causal_topk_row_blocked (:132-171) and
+ *           _finalize_causal_topk (:37-57).
+ * query, key : (B, T, R) of `dtype`, element strides q_strides[3], k_strides[3].
+ * out_idx    : (B, T, k_eff) int32, contiguous, k_eff = min(top_k, T).
+ *              Row t holds the k_eff keys j <= t with the largest fp32 scores
+ *              s(t, j) = fma-chain over d of query[t,d]*key[j,d] (d ascending, fp32),
+ *              ties resolved to the lower j. Rows with t+1 < k_eff hold their t+1 causal
+ *              keys in slots 0..t and pad index (t + k_eff + s + 1) % T in slot s > t.
+ * out_scores : optional (B, T, k_eff) float32 (NULL to skip): the fp32 score of every
+ *              slot, -inf in pad slots.
+ * workspace  : device buffer of at least wf_causal_topk_workspace_bytes(...) bytes.
+ * Limits: 1 <= R <= 128, 1 <= top_k (k_eff <= 256), T < 2^31.
+ */
+int wf_causal_topk_fwd(const void* query, const void* key, int dtype,
+                       int64_t B, int64_t T, int64_t R,
+                       const int64_t* q_strides, const int64_t* k_strides,
+                       int64_t top_k, int32_t* out_idx, float* out_scores,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse attention readout over pre-selected indices, shared across heads.
+ * Replaces: sparse_meat_attention (routing_attention/kernels/fused_sparse.py:275-324),
+ *           i.e. _sparse_meat_batched (:97-128) / sparse_meat_attention_reference (:80-94).
+ * q, k, v  : (B, H, T, D) of `dtype`, element strides *_strides[4] (any layout; the
+ *            (B,T,H,D) memory of a .view(B,T,H,D).transpose(1,2) is the fast case).
+ * indices  : (B, T, K) int32, strides idx_strides[3]. Negative entries wrap (+T) as in
+ *            torch advanced indexing; entries outside [-T, T) are clamped to [0, T-1].
+ * out      : (B, H, T, D) of `dtype`, strides out_strides[4]:
+ *            out[b,h,t] = sum_s softmax_s(scale * q[b,h,t].k[b,h,idx[b,t,s]]) v[b,h,idx[b,t,s]]
+ *            computed in fp32, rounded once to `dtype`.
+ * flags    : WF_FLAG_MASK_PADS or 0.
+ * Limits: D in {32, 64, 128}, 1 <= K <= 1024.
+ */
+int wf_sparse_readout_fwd(const void* q, const void* k, const void* v, int dtype,
+                          int64_t B, int64_t H, int64_t T, int64_t D,
+                          const int64_t* q_strides, const int64_t* k_strides,
+                          const int64_t* v_strides,
+                          const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                          float scale, unsigned flags,
+                          void* out, const int64_t* out_strides, void* stream);
+
+/* Arguments of the fused forward, one struct so the entry point stays stable. */
+typedef struct wf_fused_args {
+    const void* q_search;       /* (B, T, R) addresses, strides qs_strides  */
+    const void* k_search;       /* (B, T, R) addresses, strides ks_strides  */
+    const void* q;              /* (B, H, T, D), strides q_strides          */
+    const void* k;
+    const void* v;
+    void* out;                  /* (B, H, T, D), strides out_strides        */
+    int32_t* out_idx;           /* (B, T, k_eff) int32 contiguous           */
+    float* out_scores;          /* optional (B, T, k_eff) fp32, or NULL     */
+    void* workspace;            /* >= wf_fused_workspace_bytes(...)         */
+    size_t workspace_bytes;
+    int64_t qs_strides[3];
+    int64_t ks_strides[3];
+    int64_t q_strides[4];
+    int64_t k_strides[4];
+    int64_t v_strides[4];
+    int64_t out_strides[4];
+    int64_t B, H, T, D, R, top_k;
+    int search_dtype;           /* wf_dtype of q_search/k_search */
+    int dtype;                  /* wf_dtype of q/k/v/out         */
+    float scale;
+    unsigned flags;             /* WF_FLAG_* */
+} wf_fused_args;
+
+size_t wf_fused_workspace_bytes(int64_t B, int64_t T, int64_t R, int64_t top_k);
+
+/*
+ * Fused causal top-K retrieval + sparse attention forward.
+ * Replaces: fused_sparse_attention (routing_attention/kernels/fused_sparse.py:327-356):
+ *           causal_topk(q_search, k_search, top_k) then sparse_meat_attention(q, k, v,
+ *           indices, scale); writes both the output and the indices.
+ */
+int wf_fused_topk_sparse_fwd(const wf_fused_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WAYFINDER_HIP_H */

@@ -1,0 +1,185 @@
+/*
+ * wf_oracle.c -- CPU restatement of Wayfinder's causal top-K retrieval and sparse
+ * attention readout.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the parity checker for libwayfinder_hip.so.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it;
+ * the product package never does.
+ *
+ * What it restates (reference = /root/reference, pure PyTorch):
+ *  - wfo_causal_topk_rows: causal_topk(method="fused_causal")
+ *      routing_attention/kernels/causal_topk.py:132-171 (_causal_topk_row_blocked: fp32
+ *      scores q.k for j <= t, top-k_eff per row) and :37-57 (_finalize_causal_topk: slots
+ *      without a causal key get pad index (t + k_eff + s + 1) % T).
+ *    The score of (t, j) is defined as the fp32 chain acc = fmaf(q[t,d], k[j,d], acc) over
+ *    d = 0..R-1 starting from acc = 0, on inputs converted exactly to fp32 (the reference
+ *    casts to fp32 at causal_topk.py:150-151 and lets torch.bmm pick the summation order).
+ *    Ties resolve to the lower key index (the north-star rule; the reference's only
+ *    explicit tie semantic, the Triton heap at causal_topk.py:305-315 streaming keys in
+ *    ascending order, behaves the same). Output is canonical: score descending, then
+ *    index ascending; valid keys fill slots 0..n_valid-1 and pads follow, which is the
+ *    slot placement torch's GPU topk(sorted=False) gives rows whose tail is -inf.
+ *  - wfo_sparse_readout: sparse_meat_attention_reference
+ *      routing_attention/kernels/fused_sparse.py:80-94 (gather k/v at indices shared
+ *      across heads :64-77, scores = (q . k_sel) * scale, softmax, weighted sum of v_sel),
+ *    accumulated in double. Negative indices wrap by +T (torch advanced indexing);
+ *    indices outside [-T, T) are clamped to [0, T-1] (the reference raises there).
+ *
+ * Build: oracle/Makefile -> oracle/libwf_oracle.so (gcc, OpenMP over rows).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* fp32 score of one (query, key) pair: sequential fused multiply-add chain. */
+float wfo_score(const float* q, const float* k, int64_t R)
+{
+    float acc = 0.0f;
+    for (int64_t d = 0; d < R; ++d) acc = fmaf(q[d], k[d], acc);
+    return acc;
+}
+
+/* Total order used for selection: a is better than b. */
+static int better(float sa, int32_t ja, float sb, int32_t jb)
+{
+    return (sa > sb) || (sa == sb && ja < jb);
+}
+
+typedef struct { float s; int32_t j; } cand;
+
+/* min-heap by "better": root is the worst kept candidate */
+static void sift_down(cand* h, int64_t n, int64_t i)
+{
+    for (;;) {
+        int64_t l = 2 * i + 1, r = l + 1, w = i;
+        if (l < n && better(h[w].s, h[w].j, h[l].s, h[l].j)) w = l;
+        if (r < n && better(h[w].s, h[w].j, h[r].s, h[r].j)) w = r;
+        if (w == i) return;
+        cand t = h[i]; h[i] = h[w]; h[w] = t; i = w;
+    }
+}
+
+static int cmp_desc(const void* pa, const void* pb)
+{
+    const cand* a = (const cand*)pa;
+    const cand* b = (const cand*)pb;
+    if (better(a->s, a->j, b->s, b->j)) return -1;
+    if (better(b->s, b->j, a->s, a->j)) return 1;
+    return 0;
+}
+
+/*
+ * Rows [row0, row1) of batch b. qa, ka: contiguous (B, T, R) fp32.
+ * out_idx / out_score: contiguous (row1 - row0, k_eff); out_score may be NULL.
+ */
+void wfo_causal_topk_rows(const float* qa, const float* ka, int64_t B, int64_t T, int64_t R,
+                          int64_t top_k, int64_t b, int64_t row0, int64_t row1,
+                          int32_t* out_idx, float* out_score)
+{
+    (void)B;
+    const int64_t k_eff = top_k < T ? top_k : T;
+    if (k_eff <= 0) return;
+#pragma omp parallel
+    {
+        cand* heap = (cand*)malloc(sizeof(cand) * (size_t)k_eff);
+#pragma omp for schedule(dynamic, 16)
+        for (int64_t t = row0; t < row1; ++t) {
+            const float* q = qa + (b * T + t) * R;
+            int64_t n = 0;
+            for (int64_t j = 0; j <= t; ++j) {
+                const float s = wfo_score(q, ka + (b * T + j) * R, R);
+                if (n < k_eff) {
+                    /* insert and restore heap order upward */
+                    int64_t i = n++;
+                    heap[i].s = s; heap[i].j = (int32_t)j;
+                    while (i > 0) {
+                        int64_t p = (i - 1) / 2;
+                        if (better(heap[p].s, heap[p].j, heap[i].s, heap[i].j)) {
+                            cand tmp = heap[p]; heap[p] = heap[i]; heap[i] = tmp; i = p;
+                        } else break;
+                    }
+                } else if (better(s, (int32_t)j, heap[0].s, heap[0].j)) {
+                    heap[0].s = s; heap[0].j = (int32_t)j;
+                    sift_down(heap, n, 0);
+                }
+            }
+            qsort(heap, (size_t)n, sizeof(cand), cmp_desc);
+            int32_t* oi = out_idx + (t - row0) * k_eff;
+            float* os = out_score ? out_score + (t - row0) * k_eff : NULL;
+            for (int64_t s = 0; s < k_eff; ++s) {
+                if (s < n) {
+                    oi[s] = heap[s].j;
+                    if (os) os[s] = heap[s].s;
+                } else {
+                    oi[s] = (int32_t)((t + k_eff + s + 1) % T);
+                    if (os) os[s] = -INFINITY;
+                }
+            }
+        }
+        free(heap);
+    }
+}
+
+/* All rows of all batches: out_idx / out_score contiguous (B, T, k_eff). */
+void wfo_causal_topk(const float* qa, const float* ka, int64_t B, int64_t T, int64_t R,
+                     int64_t top_k, int32_t* out_idx, float* out_score)
+{
+    const int64_t k_eff = top_k < T ? top_k : T;
+    for (int64_t b = 0; b < B; ++b)
+        wfo_causal_topk_rows(qa, ka, B, T, R, top_k, b, 0, T, out_idx + b * T * k_eff,
+                             out_score ? out_score + b * T * k_eff : NULL);
+}
+
+/*
+ * q, k, v: contiguous (B, H, T, D) fp32; idx: contiguous (B, T, K) int32;
+ * out: contiguous (B, H, T, D) double. flags bit 0: zero weight for slots s > t of
+ * rows t < K - 1 (pad slots of the retrieval).
+ */
+void wfo_sparse_readout(const float* q, const float* k, const float* v,
+                        int64_t B, int64_t H, int64_t T, int64_t D,
+                        const int32_t* idx, int64_t K, float scale, unsigned flags,
+                        double* out)
+{
+#pragma omp parallel
+    {
+        double* sc = (double*)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
+        int64_t* jj = (int64_t*)malloc(sizeof(int64_t) * (size_t)(K > 0 ? K : 1));
+#pragma omp for collapse(2) schedule(static)
+        for (int64_t bh = 0; bh < B * H; ++bh) {
+            for (int64_t t = 0; t < T; ++t) {
+                const int64_t b = bh / H;
+                const float* qr = q + (bh * T + t) * D;
+                const int32_t* ir = idx + (b * T + t) * K;
+                double m = -INFINITY;
+                for (int64_t s = 0; s < K; ++s) {
+                    int64_t j = ir[s];
+                    if (j < 0) j += T;
+                    if (j < 0) j = 0;
+                    if (j > T - 1) j = T - 1;
+                    jj[s] = j;
+                    const int masked = (flags & 1u) && t < K - 1 && s > t;
+                    if (masked) { sc[s] = -INFINITY; continue; }
+                    const float* kr = k + (bh * T + j) * D;
+                    double dot = 0.0;
+                    for (int64_t d = 0; d < D; ++d) dot += (double)qr[d] * (double)kr[d];
+                    sc[s] = dot * (double)scale;
+                    if (sc[s] > m) m = sc[s];
+                }
+                double* orow = out + (bh * T + t) * D;
+                for (int64_t d = 0; d < D; ++d) orow[d] = 0.0;
+                double l = 0.0;
+                for (int64_t s = 0; s < K; ++s) {
+                    if (sc[s] == -INFINITY) continue;
+                    const double p = exp(sc[s] - m);
+                    l += p;
+                    const float* vr = v + (bh * T + jj[s]) * D;
+                    for (int64_t d = 0; d < D; ++d) orow[d] += p * (double)vr[d];
+                }
+                for (int64_t d = 0; d < D; ++d) orow[d] = l > 0.0 ? orow[d] / l : 0.0;
+            }
+        }
+        free(sc);
+        free(jj);
+    }
+}

@@ -1,0 +1,146 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the public header
+declares, and reports contract violations as status codes before any HIP call."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from routing_attention.kernels import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "wayfinder_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(wf_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_declares_the_abi():
+    names = _declared()
+    assert names == sorted(_lib.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.wf_abi_version() == _lib.ABI_VERSION == 1
+
+
+def _i64(*v):
+    return (ctypes.c_int64 * len(v))(*v)
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def _topk(lib, **kw):
+    a = dict(query=FAKE, key=FAKE, dtype=2, B=1, T=64, R=32, qs=_i64(64 * 32, 32, 1),
+             ks=_i64(64 * 32, 32, 1), top_k=8, out=FAKE, scores=None, ws=FAKE, ws_bytes=1 << 20)
+    a.update(kw)
+    return lib.wf_causal_topk_fwd(a["query"], a["key"], a["dtype"], a["B"], a["T"], a["R"],
+                                  a["qs"], a["ks"], a["top_k"], a["out"], a["scores"], a["ws"],
+                                  a["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=9), _lib.WF_ERR_UNSUPPORTED, "dtype"),
+    (dict(R=0), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
+    (dict(T=-1), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
+    (dict(top_k=-3), _lib.WF_ERR_INVALID_ARGUMENT, "top_k"),
+    (dict(R=129), _lib.WF_ERR_UNSUPPORTED, "R=129"),
+    (dict(top_k=300, T=1000), _lib.WF_ERR_UNSUPPORTED, "k_eff"),
+    (dict(query=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(out=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(qs=None), _lib.WF_ERR_INVALID_ARGUMENT, "stride"),
+    (dict(ws=None), _lib.WF_ERR_WORKSPACE, "workspace"),
+    (dict(ws_bytes=4), _lib.WF_ERR_WORKSPACE, "workspace"),
+])
+def test_topk_contract_errors(lib, kw, code, msg):
+    assert _topk(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_topk_empty_problems_are_noops(lib):
+    assert _topk(lib, B=0) == _lib.WF_OK
+    assert _topk(lib, top_k=0) == _lib.WF_OK
+    assert _topk(lib, T=0) == _lib.WF_OK
+    assert _lib.last_error() == ""
+
+
+def test_workspace_size(lib):
+    assert lib.wf_causal_topk_workspace_bytes(1, 16384, 32, 128) == 256
+    assert lib.wf_causal_topk_workspace_bytes(4, 65536, 32, 256) == 4 * 256 * 4
+    assert lib.wf_causal_topk_workspace_bytes(0, 10, 32, 8) == 0
+    assert lib.wf_fused_workspace_bytes(2, 1000, 32, 8) == lib.wf_causal_topk_workspace_bytes(2, 1000, 32, 8)
+
+
+def _readout(lib, **kw):
+    s4 = _i64(8 * 64 * 64, 64 * 64, 64, 1)
+    a = dict(q=FAKE, k=FAKE, v=FAKE, dtype=2, B=1, H=8, T=64, D=64, qs=s4, ks=s4, vs=s4,
+             idx=FAKE, is_=_i64(64 * 8, 8, 1), K=8, scale=0.125, flags=0, out=FAKE, os=s4)
+    a.update(kw)
+    return lib.wf_sparse_readout_fwd(a["q"], a["k"], a["v"], a["dtype"], a["B"], a["H"], a["T"],
+                                     a["D"], a["qs"], a["ks"], a["vs"], a["idx"], a["is_"], a["K"],
+                                     a["scale"], a["flags"], a["out"], a["os"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=-1), _lib.WF_ERR_UNSUPPORTED, "dtype"),
+    (dict(D=48), _lib.WF_ERR_UNSUPPORTED, "head_dim"),
+    (dict(K=0), _lib.WF_ERR_INVALID_ARGUMENT, "K must"),
+    (dict(K=5000), _lib.WF_ERR_UNSUPPORTED, "K=5000"),
+    (dict(H=-2), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
+    (dict(v=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(idx=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(os=None), _lib.WF_ERR_INVALID_ARGUMENT, "stride"),
+])
+def test_readout_contract_errors(lib, kw, code, msg):
+    assert _readout(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_readout_empty_is_noop(lib):
+    assert _readout(lib, T=0) == _lib.WF_OK
+
+
+def test_fused_contract_errors(lib):
+    assert lib.wf_fused_topk_sparse_fwd(None, None) == _lib.WF_ERR_INVALID_ARGUMENT
+    a = _lib.FusedArgs()
+    a.q_search = a.k_search = a.q = a.k = a.v = a.out = a.out_idx = FAKE
+    a.workspace, a.workspace_bytes = FAKE, 1 << 20
+    a.qs_strides[:] = [64 * 32, 32, 1]
+    a.ks_strides[:] = [64 * 32, 32, 1]
+    for f in ("q_strides", "k_strides", "v_strides", "out_strides"):
+        getattr(a, f)[:] = [8 * 64 * 64, 64 * 64, 64, 1]
+    a.B, a.H, a.T, a.D, a.R, a.top_k = 1, 8, 64, 64, 32, 8
+    a.search_dtype, a.dtype, a.scale = 2, 2, 0.125
+    a.D = 40
+    assert lib.wf_fused_topk_sparse_fwd(ctypes.byref(a), None) == _lib.WF_ERR_UNSUPPORTED
+    a.D, a.top_k = 64, 0
+    assert lib.wf_fused_topk_sparse_fwd(ctypes.byref(a), None) == _lib.WF_ERR_INVALID_ARGUMENT
+    a.top_k, a.workspace_bytes = 8, 0
+    assert lib.wf_fused_topk_sparse_fwd(ctypes.byref(a), None) == _lib.WF_ERR_WORKSPACE
+
+
+def test_status_maps_to_reference_exception_types():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.WF_ERR_INVALID_ARGUMENT)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.WF_ERR_UNSUPPORTED)
+    with pytest.raises(_lib.WayfinderHipError):
+        _lib.check(_lib.WF_ERR_HIP)
+    _lib.check(_lib.WF_OK)

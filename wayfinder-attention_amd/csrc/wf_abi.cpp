@@ -1,0 +1,237 @@
+// wf_abi.cpp -- extern "C" entry points of libwayfinder_hip.so (declared in
+// include/wayfinder_hip.h): argument validation, workspace sizing, kernel dispatch and
+// error reporting. Validation runs before any HIP call, so contract errors surface as
+// status codes on machines without a GPU too.
+#include "wayfinder_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "wf_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok()
+{
+    g_last_error.clear();
+    return WF_OK;
+}
+
+size_t elem_size(int dtype) { return dtype == WF_DTYPE_F32 ? 4 : 2; }
+
+bool valid_dtype(int dtype)
+{
+    return dtype == WF_DTYPE_F32 || dtype == WF_DTYPE_F16 || dtype == WF_DTYPE_BF16;
+}
+
+// 16-byte vector access is legal for every row when the innermost stride is 1, the row
+// length is a multiple of 8 elements and every other stride and the base keep 16-byte
+// alignment.
+bool vec_ok(const void* base, int dtype, const int64_t* strides, int ndim, int64_t inner)
+{
+    const size_t es = elem_size(dtype);
+    if (strides[ndim - 1] != 1 || inner % 8 != 0) return false;
+    if (reinterpret_cast<uintptr_t>(base) % 16 != 0) return false;
+    for (int i = 0; i < ndim - 1; ++i)
+        if ((strides[i] * int64_t(es)) % 16 != 0) return false;
+    return true;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int64_t gcd64(int64_t a, int64_t b)
+{
+    while (b) { const int64_t t = a % b; a = b; b = t; }
+    return a;
+}
+
+constexpr int64_t kMaxTopK = 256;
+constexpr int64_t kMaxR = 128;
+constexpr int64_t kMaxReadoutK = 1024;
+
+int check_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T, int64_t R,
+               const int64_t* qs, const int64_t* ks, int64_t top_k, const int32_t* out_idx)
+{
+    if (!valid_dtype(dtype)) return fail(WF_ERR_UNSUPPORTED, "causal_topk: unsupported dtype code %d", dtype);
+    if (B < 0 || T < 0 || R < 1) return fail(WF_ERR_INVALID_ARGUMENT, "causal_topk: bad shape (B=%lld, T=%lld, R=%lld)", (long long)B, (long long)T, (long long)R);
+    if (top_k < 0) return fail(WF_ERR_INVALID_ARGUMENT, "causal_topk: top_k must be >= 0, got %lld", (long long)top_k);
+    if (T >= (int64_t(1) << 31) - 1) return fail(WF_ERR_UNSUPPORTED, "causal_topk: T=%lld does not fit int32 indices", (long long)T);
+    if (R > kMaxR) return fail(WF_ERR_UNSUPPORTED, "causal_topk: address dim R=%lld > %lld", (long long)R, (long long)kMaxR);
+    if (!qs || !ks) return fail(WF_ERR_INVALID_ARGUMENT, "causal_topk: stride arrays must not be NULL");
+    const int64_t k_eff = std::min(top_k, T);
+    if (k_eff > kMaxTopK) return fail(WF_ERR_UNSUPPORTED, "causal_topk: k_eff=%lld > %lld", (long long)k_eff, (long long)kMaxTopK);
+    if (B > 0 && k_eff > 0 && (!query || !key || !out_idx))
+        return fail(WF_ERR_INVALID_ARGUMENT, "causal_topk: NULL query/key/out_idx pointer");
+    return WF_OK;
+}
+
+int check_readout(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                  int64_t T, int64_t D, const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                  const int32_t* idx, const int64_t* is, int64_t K, const void* out,
+                  const int64_t* os)
+{
+    if (!valid_dtype(dtype)) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: unsupported dtype code %d", dtype);
+    if (B < 0 || H < 0 || T < 0 || D < 1) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout: bad shape (B=%lld, H=%lld, T=%lld, D=%lld)", (long long)B, (long long)H, (long long)T, (long long)D);
+    if (D != 32 && D != 64 && D != 128) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: head_dim %lld not in {32, 64, 128}", (long long)D);
+    if (K < 1) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout: K must be >= 1, got %lld", (long long)K);
+    if (K > kMaxReadoutK) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: K=%lld > %lld", (long long)K, (long long)kMaxReadoutK);
+    if (T >= (int64_t(1) << 31) - 1) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: T=%lld does not fit int32 indices", (long long)T);
+    if (!qs || !ks || !vs || !is || !os) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout: stride arrays must not be NULL");
+    if (B * H * T > 0 && (!q || !k || !v || !idx || !out))
+        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout: NULL tensor pointer");
+    return WF_OK;
+}
+
+int hip_fail(const char* what, hipError_t e)
+{
+    return fail(WF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T, int64_t R,
+             const int64_t* qs, const int64_t* ks, int64_t top_k, int32_t* out_idx,
+             float* out_scores, void* ws, size_t ws_bytes, hipStream_t stream)
+{
+    const int64_t k_eff = std::min(top_k, T);
+    if (B == 0 || k_eff == 0) return WF_OK;
+    const size_t need = wf_causal_topk_workspace_bytes(B, T, R, top_k);
+    if (!ws || ws_bytes < need)
+        return fail(WF_ERR_WORKSPACE, "causal_topk: workspace of %zu bytes required, got %zu", need, ws ? ws_bytes : size_t(0));
+    if (reinterpret_cast<uintptr_t>(ws) % 4 != 0) return fail(WF_ERR_INVALID_ARGUMENT, "causal_topk: workspace not 4-byte aligned");
+    wf::TopkParams p{};
+    p.query = query; p.key = key;
+    p.qsb = qs[0]; p.qst = qs[1]; p.qsr = qs[2];
+    p.ksb = ks[0]; p.kst = ks[1]; p.ksr = ks[2];
+    p.B = B; p.T = T; p.R = R; p.k_eff = k_eff;
+    p.out_idx = out_idx; p.out_scores = out_scores;
+    p.chunk_absmax = static_cast<float*>(ws);
+    p.n_chunks = cdiv(T, wf::kAbsmaxChunk);
+    p.n_row_blocks = cdiv(T, 16);
+    const bool vec = vec_ok(query, dtype, qs, 3, R) && vec_ok(key, dtype, ks, 3, R);
+    hipError_t e = wf::launch_key_absmax(dtype, p, stream);
+    if (e != hipSuccess) return hip_fail("causal_topk: key magnitude kernel launch", e);
+    e = wf::launch_causal_topk(dtype, vec, p, stream);
+    if (e != hipSuccess) return hip_fail("causal_topk: retrieval kernel launch", e);
+    return WF_OK;
+}
+
+int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                int64_t T, int64_t D, const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                const int32_t* idx, const int64_t* is, int64_t K, float scale, unsigned flags,
+                void* out, const int64_t* os, hipStream_t stream)
+{
+    if (B * H * T == 0) return WF_OK;
+    wf::ReadoutParams p{};
+    p.q = q; p.k = k; p.v = v; p.out = out; p.idx = idx;
+    for (int i = 0; i < 4; ++i) { p.qs[i] = qs[i]; p.ks[i] = ks[i]; p.vs[i] = vs[i]; p.os[i] = os[i]; }
+    for (int i = 0; i < 3; ++i) p.is[i] = is[i];
+    p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
+    p.scale = scale; p.flags = flags;
+    // split each (b, h) pair into row segments so that the number of virtual pairs is a
+    // multiple of the 8 XCDs
+    const int64_t nbh = B * H;
+    p.seg_per_pair = 8 / gcd64(nbh, 8);
+    p.rows_per_seg = cdiv(T, p.seg_per_pair);
+    p.vpairs = nbh * p.seg_per_pair;
+    p.wg_per_vpair = cdiv(p.rows_per_seg, 4);
+    const int64_t grid = p.vpairs * p.wg_per_vpair;
+    if (grid >= (int64_t(1) << 31)) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: problem too large for one launch");
+    const bool vec = vec_ok(q, dtype, qs, 4, D) && vec_ok(k, dtype, ks, 4, D) &&
+                     vec_ok(v, dtype, vs, 4, D) && vec_ok(out, dtype, os, 4, D);
+    const hipError_t e = wf::launch_sparse_readout(dtype, vec, p, stream);
+    if (e != hipSuccess) return hip_fail("sparse_readout: kernel launch", e);
+    return WF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wf_abi_version(void) { return WF_ABI_VERSION; }
+
+const char* wf_last_error(void) { return g_last_error.c_str(); }
+
+size_t wf_causal_topk_workspace_bytes(int64_t B, int64_t T, int64_t R, int64_t top_k)
+{
+    (void)R;
+    (void)top_k;
+    if (B <= 0 || T <= 0) return 0;
+    return align256(size_t(B) * size_t(cdiv(T, wf::kAbsmaxChunk)) * sizeof(float));
+}
+
+size_t wf_fused_workspace_bytes(int64_t B, int64_t T, int64_t R, int64_t top_k)
+{
+    return wf_causal_topk_workspace_bytes(B, T, R, top_k);
+}
+
+int wf_causal_topk_fwd(const void* query, const void* key, int dtype, int64_t B, int64_t T,
+                       int64_t R, const int64_t* q_strides, const int64_t* k_strides,
+                       int64_t top_k, int32_t* out_idx, float* out_scores, void* workspace,
+                       size_t workspace_bytes, void* stream)
+{
+    int rc = check_topk(query, key, dtype, B, T, R, q_strides, k_strides, top_k, out_idx);
+    if (rc != WF_OK) return rc;
+    rc = run_topk(query, key, dtype, B, T, R, q_strides, k_strides, top_k, out_idx, out_scores,
+                  workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+    return rc == WF_OK ? ok() : rc;
+}
+
+int wf_sparse_readout_fwd(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                          int64_t H, int64_t T, int64_t D, const int64_t* q_strides,
+                          const int64_t* k_strides, const int64_t* v_strides,
+                          const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                          float scale, unsigned flags, void* out, const int64_t* out_strides,
+                          void* stream)
+{
+    int rc = check_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
+                           idx_strides, K, out, out_strides);
+    if (rc != WF_OK) return rc;
+    rc = run_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
+                     idx_strides, K, scale, flags, out, out_strides, static_cast<hipStream_t>(stream));
+    return rc == WF_OK ? ok() : rc;
+}
+
+int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
+{
+    if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "fused: NULL argument struct");
+    int rc = check_topk(a->q_search, a->k_search, a->search_dtype, a->B, a->T, a->R,
+                        a->qs_strides, a->ks_strides, a->top_k, a->out_idx);
+    if (rc != WF_OK) return rc;
+    const int64_t k_eff = std::min(a->top_k, a->T);
+    if (k_eff < 1 && a->B * a->T > 0)
+        return fail(WF_ERR_INVALID_ARGUMENT, "fused: top_k must be >= 1 (empty selections have no readout)");
+    const int64_t is[3] = {a->T * k_eff, k_eff, 1};
+    rc = check_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
+                       a->k_strides, a->v_strides, a->out_idx, is, k_eff > 0 ? k_eff : 1, a->out,
+                       a->out_strides);
+    if (rc != WF_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = run_topk(a->q_search, a->k_search, a->search_dtype, a->B, a->T, a->R, a->qs_strides,
+                  a->ks_strides, a->top_k, a->out_idx, a->out_scores, a->workspace,
+                  a->workspace_bytes, s);
+    if (rc != WF_OK) return rc;
+    rc = run_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
+                     a->k_strides, a->v_strides, a->out_idx, is, k_eff, a->scale, a->flags,
+                     a->out, a->out_strides, s);
+    return rc == WF_OK ? ok() : rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+// wf_internal.h -- device helpers and launcher declarations shared by the gfx950 kernels
+// of libwayfinder_hip.so. Not part of the public ABI (include/wayfinder_hip.h is).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wf {
+
+// ---------------------------------------------------------------- element types
+// bf16 is carried as its raw 16-bit pattern; f16 as _Float16; f32 as float.
+struct bf16_t { uint16_t bits; };
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float(uint32_t(x.bits) << 16); }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(float x) { return x; }
+
+// round-to-nearest-even fp32 -> storage type (NaN kept quiet)
+__device__ __forceinline__ void from_f32(float x, bf16_t& y)
+{
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) { y.bits = uint16_t((u >> 16) | 0x40u); return; }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    y.bits = uint16_t(u >> 16);
+}
+__device__ __forceinline__ void from_f32(float x, _Float16& y) { y = (_Float16)x; }
+__device__ __forceinline__ void from_f32(float x, float& y) { y = x; }
+
+// Raw 16-byte chunk <-> eight fp32 values (bf16 / f16: one chunk = 8 elements).
+__device__ __forceinline__ void unpack8(const uint4& u, bf16_t, float* f)
+{
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ void unpack8(const uint4& u, _Float16, float* f)
+{
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        _Float16 lo = __builtin_bit_cast(_Float16, uint16_t(w[i] & 0xffffu));
+        _Float16 hi = __builtin_bit_cast(_Float16, uint16_t(w[i] >> 16));
+        f[2 * i] = (float)lo;
+        f[2 * i + 1] = (float)hi;
+    }
+}
+
+// ---------------------------------------------------------------- wave helpers (wave64)
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ float wave_max(float x)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint32_t y = __shfl_xor(x, o, 64);
+        x = y < x ? y : x;
+    }
+    return x;
+}
+// sum over lanes with index > lane (exclusive suffix sum)
+__device__ __forceinline__ int wave_suffix_excl(int x)
+{
+    const int lane = lane_id();
+    int s = x;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        int y = __shfl_down(s, o, 64);
+        if (lane + o < 64) s += y;
+    }
+    return s - x;
+}
+
+// order-preserving map fp32 -> uint32 (larger float -> larger uint); -0 is folded to +0
+__device__ __forceinline__ uint32_t ord_f32(float s)
+{
+    uint32_t u = __float_as_uint(s + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float unord_f32(uint32_t o)
+{
+    uint32_t u = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
+    return __uint_as_float(u);
+}
+
+// ---------------------------------------------------------------- launch parameter blocks
+struct TopkParams {
+    const void* query;
+    const void* key;
+    int64_t qsb, qst, qsr;   // element strides of query (B, T, R)
+    int64_t ksb, kst, ksr;   // element strides of key
+    int64_t B, T, R, k_eff;
+    int32_t* out_idx;        // (B, T, k_eff) contiguous
+    float* out_scores;       // optional
+    float* chunk_absmax;     // (B, n_chunks) workspace
+    int64_t n_chunks;
+    int64_t n_row_blocks;    // ceil(T / 16)
+};
+
+struct ReadoutParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    const int32_t* idx;
+    int64_t qs[4], ks[4], vs[4], os[4];  // element strides (B, H, T, D)
+    int64_t is[3];                       // index strides (B, T, K)
+    int64_t B, H, T, D, K;
+    float scale;
+    unsigned flags;
+    int64_t seg_per_pair;   // row segments per (b,h) pair (XCD balance)
+    int64_t rows_per_seg;
+    int64_t vpairs;         // B*H*seg_per_pair virtual pairs
+    int64_t wg_per_vpair;   // workgroups per virtual pair
+};
+
+// Key-magnitude chunk size of the screening bound (keys per chunk).
+constexpr int kAbsmaxChunk = 256;
+
+// launchers (return hipError_t of the launch)
+hipError_t launch_key_absmax(int dtype, const TopkParams& p, hipStream_t s);
+hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s);
+hipError_t launch_sparse_readout(int dtype, bool vec, const ReadoutParams& p, hipStream_t s);
+
+}  // namespace wf
