@@ -126,7 +126,7 @@ int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T
     p.n_chunks = cdiv(T, wf::kAbsmaxChunk);
     p.n_row_blocks = cdiv(T, 16);
     const bool vec = vec_ok(query, dtype, qs, 3, R) && vec_ok(key, dtype, ks, 3, R);
-    hipError_t e = wf::launch_key_absmax(dtype, p, stream);
+    hipError_t e = wf::launch_key_absmax(dtype, vec, p, stream);
     if (e != hipSuccess) return hip_fail("causal_topk: key magnitude kernel launch", e);
     e = wf::launch_causal_topk(dtype, vec, p, stream);
     if (e != hipSuccess) return hip_fail("causal_topk: retrieval kernel launch", e);

@@ -130,7 +130,7 @@ struct ReadoutParams {
 constexpr int kAbsmaxChunk = 256;
 
 // launchers (return hipError_t of the launch)
-hipError_t launch_key_absmax(int dtype, const TopkParams& p, hipStream_t s);
+hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_sparse_readout(int dtype, bool vec, const ReadoutParams& p, hipStream_t s);
 

@@ -3,32 +3,40 @@
 // Replaces routing_attention/kernels/causal_topk.py:132-171 (_causal_topk_row_blocked) and
 // :37-57 (_finalize_causal_topk). Where the reference writes a (B, block_m, i1) fp32 score
 // block to HBM per row block and runs torch.topk over it, this kernel never materialises
-// scores outside LDS:
+// scores outside LDS. One workgroup = 4 waves = one block of 16 query rows:
 //
-//  1. screen   One wave owns 16 query rows. It streams the causal key prefix 16 keys at a
-//              time; one v_mfma_f32_16x16x32_{bf16,f16} (or eight 16x16x4 f32) per 32
-//              address dims scores the 16x16 tile. A key is kept as a candidate of a row
-//              only if its MFMA score reaches that row's threshold: the exact K-th best
-//              score so far minus eps, where eps bounds |MFMA score - exact score|.
-//  2. pool     Candidates are appended (LDS atomics) to a per-row pool in LDS that holds
-//              the current exact top-K plus pending candidate indices.
-//  3. compact  When a pool fills up, the wave rescores the pending candidates exactly
-//              (fp32 fma chain over d ascending, the oracle's definition of the score),
-//              radix-selects the K best under (score desc, index asc) and raises the
-//              row's threshold.
-//  4. emit     After the prefix is exhausted, each row's top-K is bitonic-sorted into
-//              canonical order and written with the reference's pad indices.
+//  1. screen   The 4 waves split the block's causal key prefix into 16-key steps (wave w
+//              takes steps w, w+4, ...). One v_mfma_f32_16x16x32_{bf16,f16} (eight
+//              16x16x4 f32 for fp32 inputs) per 32 address dims scores a 16 keys x 16 rows
+//              tile. A key becomes a candidate of a row when its MFMA score reaches the
+//              row's screening threshold; candidates (MFMA score, key) are appended with
+//              LDS atomics to the row's pool, shared by the 4 waves.
+//  2. prune    When a pool is nearly full (checked at a workgroup barrier after every
+//              step), all 16 rows are pruned in parallel, 16 lanes per row: a 128-bin
+//              histogram of the pool's MFMA scores gives a value theta' with at least K
+//              entries above it; entries below theta' - 2 eps are dropped and the row's
+//              threshold becomes theta' - 2 eps. eps bounds |MFMA score - exact score|.
+//  3. exact    At the end (or when near-ties keep a pool from shrinking) the pool is
+//              rescored exactly -- fp32 fma chain over the address dims in ascending
+//              order, the oracle's definition of the score -- and the K best under
+//              (score desc, index asc) are radix-selected from the 64-bit keys.
+//  4. emit     The K winners are bitonic-sorted into canonical order and written with
+//              the reference's pad indices for rows that have fewer than K causal keys.
 //
-// The selection is exact: a key that belongs to the final top-K has exact score > the
-// current K-th score (ties lose to the lower, earlier index), so its MFMA score is at
-// least threshold - eps and it reaches the pool; the final choice uses exact scores only.
+// Exactness: let E be the exact top-K of the keys seen so far and s_K its K-th score. The
+// pool always contains E: a pool holding K entries with MFMA score >= theta' has exact
+// K-th score >= theta' - eps, so s_K >= theta' - eps and every key that can still enter E
+// (exact score >= s_K, ties included since waves see keys out of index order) has MFMA
+// score >= theta' - 2 eps = the threshold. The final choice uses exact scores only.
 #include "wf_internal.h"
 
 namespace wf {
 namespace {
 
-constexpr int kRows = 16;                              // query rows per wave (MFMA N)
-constexpr int kPrefetch = 8;                           // key steps loaded ahead
+constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
+constexpr int kWaves = 4;                              // waves per workgroup (split the keys)
+constexpr int kBins = 128;                             // pruning histogram bins per row
+constexpr int kPrefetch = 4;                           // key steps each wave loads ahead
 constexpr float kEpsRel = 1.0f / 4096.0f;              // 2^-12: > 20x the MFMA/FMA error bound
 constexpr float kTiny = 7.888609052210118e-31f;        // 2^-100: covers denormal flushing
 
@@ -139,155 +147,263 @@ __device__ __forceinline__ uint64_t make_key(float s, uint32_t j)
     return (uint64_t(ord_f32(s)) << 32) | uint64_t(0xffffffffu - j);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m)
+// ------------------------------------------------------------------ 16-lane row groups
+// In the row-parallel phases query row r of the block is owned by lanes 16*(r%4)..+15 of
+// wave r/4, i.e. by one 16-lane DPP row, so all cross-lane traffic stays inside a wave.
+__device__ __forceinline__ float row_max16(float x)
 {
-    const uint32_t lo = __shfl_xor(uint32_t(x), m, 64);
-    const uint32_t hi = __shfl_xor(uint32_t(x >> 32), m, 64);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 16));
+    return x;
+}
+__device__ __forceinline__ float row_min16(float x)
+{
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o, 16));
+    return x;
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m, int width)
+{
+    const uint32_t lo = __shfl_xor(uint32_t(x), m, width);
+    const uint32_t hi = __shfl_xor(uint32_t(x >> 32), m, width);
     return (uint64_t(hi) << 32) | lo;
 }
+__device__ __forceinline__ uint64_t row_max16_u64(uint64_t x)
+{
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) { const uint64_t y = shfl_xor_u64(x, o, 16); x = y > x ? y : x; }
+    return x;
+}
+__device__ __forceinline__ uint64_t row_min16_u64(uint64_t x)
+{
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) { const uint64_t y = shfl_xor_u64(x, o, 16); x = y < x ? y : x; }
+    return x;
+}
+// sum of x over the lanes of the row with a higher sub-lane index
+__device__ __forceinline__ int row_suffix_excl16(int x, int u)
+{
+    int s = x;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        const int y = __shfl_down(s, o, 16);
+        if (u + o < 16) s += y;
+    }
+    return s - x;
+}
+__device__ __forceinline__ uint32_t row_bits16(uint64_t ballot)
+{
+    return uint32_t(ballot >> (lane_id() & 48)) & 0xffffu;
+}
 
-// ------------------------------------------------------------------ LDS layout
+struct Entry {
+    float s;      // MFMA score while pending, exact score after rescoring
+    uint32_t j;   // key index
+};
+
 template <int RP, int POOL>
 struct TopkSmem {
     float q[kRows][RP];            // fp32 query rows (exact rescoring)
-    float score[kRows][POOL];      // exact scores of kept entries / rescored pending ones
-    uint32_t idx[kRows][POOL];     // key index of every pool entry
-    uint32_t hist[256];            // radix-select histogram
-    int cnt[kRows];                // pool fill (kept + pending)
-    int kept[kRows];               // entries with exact scores that form the current top-K
-    float thr[kRows];              // screening threshold (K-th exact score - eps, or -inf)
+    Entry pool[kRows][POOL];       // candidate pool per row
+    uint32_t hist[kRows][kBins];   // per-row histogram (pruning and radix select)
+    int cnt[kRows];                // pool fill
+    float thr[kRows];              // screening threshold (-inf until K candidates are known)
     float eps[kRows];              // |MFMA score - exact score| bound of the row
 };
 
-// Rescore row r's pending entries, keep its K best, refresh its threshold.
-template <typename DT, bool VEC, int RP, int POOL>
-__device__ void compact_row(TopkSmem<RP, POOL>& sm, int r, int K, const DT* kb, int64_t kst,
-                            int64_t ksr, int R)
+// Largest bin b (of the row's kBins-bin histogram) whose suffix count C(b) reaches `need`;
+// also C(b+1) (entries strictly above) and the count of bin b.
+__device__ __forceinline__ void find_boundary(const uint32_t* hist, int u, int need, int& b,
+                                              int& gt, int& eq)
 {
-    constexpr int E = POOL / 64;
-    const int lane = lane_id();
-    const int c = sm.cnt[r];
-    const int nk = sm.kept[r];
-
-    for (int e = nk + lane; e < c; e += 64) {
-        const uint32_t j = sm.idx[r][e];
-        sm.score[r][e] = exact_score<DT, VEC>(sm.q[r], kb + int64_t(j) * kst, ksr, R);
-    }
-    __syncthreads();
-
-    uint64_t key[E];
-    float sv[E];
-    uint32_t iv[E];
-    bool val[E];
+    const uint4 h0 = reinterpret_cast<const uint4*>(hist)[2 * u];
+    const uint4 h1 = reinterpret_cast<const uint4*>(hist)[2 * u + 1];
+    const int h[8] = {int(h0.x), int(h0.y), int(h0.z), int(h0.w),
+                      int(h1.x), int(h1.y), int(h1.z), int(h1.w)};
+    int tot = 0;
 #pragma unroll
-    for (int m = 0; m < E; ++m) {
-        const int e = lane + 64 * m;
-        val[m] = e < c;
-        sv[m] = val[m] ? sm.score[r][e] : 0.0f;
-        iv[m] = val[m] ? sm.idx[r][e] : 0u;
-        key[m] = val[m] ? make_key(sv[m], iv[m]) : 0ull;
+    for (int k = 0; k < 8; ++k) tot += h[k];
+    const int above = row_suffix_excl16(tot, u);
+    const bool has = above < need && above + tot >= need;
+    int cum = above, bb = -1, g = 0, e = 0;
+#pragma unroll
+    for (int k = 7; k >= 0; --k) {
+        if (bb < 0 && cum + h[k] >= need) { bb = 8 * u + k; g = cum; e = h[k]; }
+        cum += h[k];
     }
+    const uint32_t bits = row_bits16(__ballot(has));
+    const int src = __ffs(bits) - 1;
+    b = __shfl(bb, src, 16);
+    gt = __shfl(g, src, 16);
+    eq = __shfl(e, src, 16);
+}
 
-    // MSD radix select of the K-th largest key (8-bit digits, early exit once the
-    // boundary bucket is taken whole). Keys are unique (distinct indices).
+// Entry <-> 64-bit selection key: (order-preserving score bits, complemented index), so a
+// larger key is a better entry under (score desc, index asc).
+__device__ __forceinline__ Entry key_entry(uint64_t k)
+{
+    return Entry{unord_f32(uint32_t(k >> 32)), 0xffffffffu - uint32_t(k)};
+}
+
+// Histogram pruning of a row whose pool holds c > K entries. Returns false when the scores
+// are too close together to separate (the caller then rescores exactly); otherwise the
+// pool is cut to the entries >= theta' - 2 eps, c_out is the new count (uniform over the
+// row's lanes) and, from lane u == 0, cnt / thr are stored for the other waves.
+template <int POOL>
+__device__ bool prune_row(Entry (&pool)[POOL], uint32_t* hist, int c, int& c_out, int& cnt,
+                          float& thr, float eps, int K, int u)
+{
+    constexpr int EPR = POOL / 16;
+    c_out = c;
+    float s[EPR];
+    float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+    for (int m = 0; m < EPR; ++m) {
+        const int e = u + 16 * m;
+        s[m] = e < c ? pool[e].s : __builtin_nanf("");
+        if (e < c) { lo = fminf(lo, s[m]); hi = fmaxf(hi, s[m]); }
+    }
+    lo = row_min16(lo);
+    hi = row_max16(hi);
+    const float span = hi - lo;
+    if (!(span > 0.0009765625f * fmaxf(fabsf(hi), fabsf(lo))) || !(span < 3.0e38f)) return false;
+    const float inv = float(kBins) / span;
+    reinterpret_cast<uint4*>(hist)[2 * u] = make_uint4(0, 0, 0, 0);
+    reinterpret_cast<uint4*>(hist)[2 * u + 1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int m = 0; m < EPR; ++m) {
+        if (u + 16 * m >= c) continue;
+        int bin = int((s[m] - lo) * inv);
+        bin = bin < 0 ? 0 : (bin > kBins - 1 ? kBins - 1 : bin);
+        atomicAdd(&hist[bin], 1u);
+    }
+    int b, gt, eq;
+    find_boundary(hist, u, K, b, gt, eq);
+    // one bin of slack absorbs the rounding of the bin computation
+    const float theta = b >= 1 ? lo + float(b - 1) * (span / float(kBins)) : lo;
+    const float kappa = theta - 2.0f * eps;
+    // in-place stream compaction: iteration m reads entries >= 16 m and writes below them
+    int base = 0;
+    const uint32_t lt = (1u << u) - 1u;
+#pragma unroll
+    for (int m = 0; m < EPR; ++m) {
+        const int e = u + 16 * m;
+        const bool sel = e < c && s[m] >= kappa;
+        const uint32_t j = sel ? pool[e].j : 0u;
+        const uint32_t bits = row_bits16(__ballot(sel));
+        if (sel) pool[base + __popc(bits & lt)] = Entry{s[m], j};
+        base += __popc(bits);
+    }
+    c_out = base;
+    if (u == 0) { cnt = base; thr = kappa; }
+    return true;
+}
+
+// Exact rescoring of a row's c pool entries and exact selection of its min(K, c) best by
+// (score desc, index asc); the winners end up in pool[0..kept) with exact scores. Returns
+// kept (uniform over the row); lane u == 0 stores cnt and the exact threshold s_K - eps.
+template <typename DT, bool VEC, int RP, int POOL>
+__device__ int exact_row(Entry (&pool)[POOL], uint32_t* hist, int c, int& cnt, float& thr,
+                         float eps, const float* q, const DT* kb, int64_t kst, int64_t ksr, int R,
+                         int K, int u)
+{
+    constexpr int EPR = POOL / 16;
+    for (int e = u; e < c; e += 16) {
+        const uint32_t j = pool[e].j;
+        pool[e].s = exact_score<DT, VEC>(q, kb + int64_t(j) * kst, ksr, R);
+    }
+    uint64_t key[EPR];
+#pragma unroll
+    for (int m = 0; m < EPR; ++m) {
+        const int e = u + 16 * m;
+        key[m] = e < c ? make_key(pool[e].s, pool[e].j) : 0ull;   // real keys are > 0
+    }
     uint64_t prefix = 0, pmask = 0;
     if (c > K) {
-        int need = K;
-        for (int shift = 56; shift >= 0; shift -= 8) {
-            reinterpret_cast<uint4*>(sm.hist)[lane] = make_uint4(0, 0, 0, 0);
-            __syncthreads();
+        uint64_t kmax = 0, kmin = ~0ull;
 #pragma unroll
-            for (int m = 0; m < E; ++m)
-                if (val[m] && (key[m] & pmask) == prefix)
-                    atomicAdd(&sm.hist[(key[m] >> shift) & 255u], 1u);
-            __syncthreads();
-            const uint4 h = reinterpret_cast<const uint4*>(sm.hist)[lane];
-            const int s3 = int(h.w), s2 = int(h.z) + s3, s1 = int(h.y) + s2, s0 = int(h.x) + s1;
-            const int above = wave_suffix_excl(s0);
-            const bool has = above < need && s0 + above >= need;
+        for (int m = 0; m < EPR; ++m)
+            if (u + 16 * m < c) { kmax = key[m] > kmax ? key[m] : kmax; kmin = key[m] < kmin ? key[m] : kmin; }
+        kmax = row_max16_u64(kmax);
+        kmin = row_min16_u64(kmin);
+        const int top = 63 - __clzll((long long)(kmax ^ kmin));   // keys are distinct
+        pmask = top >= 63 ? 0ull : ~((2ull << top) - 1ull);
+        prefix = kmax & pmask;
+        int need = K;
+        for (int shift = top - 6; shift > -7; shift -= 7) {
+            reinterpret_cast<uint4*>(hist)[2 * u] = make_uint4(0, 0, 0, 0);
+            reinterpret_cast<uint4*>(hist)[2 * u + 1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int m = 0; m < EPR; ++m) {
+                if (u + 16 * m >= c || (key[m] & pmask) != prefix) continue;
+                const uint32_t d = shift >= 0 ? uint32_t(key[m] >> shift) & 127u
+                                              : uint32_t(key[m] << (-shift)) & 127u;
+                atomicAdd(&hist[d], 1u);
+            }
             int d, gt, eq;
-            if (s3 + above >= need) { d = 4 * lane + 3; gt = above; eq = int(h.w); }
-            else if (s2 + above >= need) { d = 4 * lane + 2; gt = above + s3; eq = int(h.z); }
-            else if (s1 + above >= need) { d = 4 * lane + 1; gt = above + s2; eq = int(h.y); }
-            else { d = 4 * lane; gt = above + s1; eq = int(h.x); }
-            const uint64_t hm = __ballot(has);
-            const int src = __ffsll((unsigned long long)hm) - 1;
-            d = __shfl(d, src, 64);
-            gt = __shfl(gt, src, 64);
-            eq = __shfl(eq, src, 64);
+            find_boundary(hist, u, need, d, gt, eq);
             need -= gt;
-            prefix |= uint64_t(d) << shift;
-            pmask |= uint64_t(0xff) << shift;
-            __syncthreads();
+            prefix |= shift >= 0 ? (uint64_t(d) << shift) : (uint64_t(d) >> (-shift));
+            pmask |= shift >= 0 ? (127ull << shift) : (127ull >> (-shift));
             if (eq == need) break;
         }
     }
-
-    // stream-compact the selected entries to the front of the pool
     int base = 0;
-    uint32_t minord = 0xffffffffu;
-    const uint64_t lt = (1ull << lane) - 1ull;
+    uint64_t kmin_sel = ~0ull;
+    const uint32_t lt = (1u << u) - 1u;
 #pragma unroll
-    for (int m = 0; m < E; ++m) {
-        const bool sel = val[m] && (key[m] & pmask) >= prefix;
-        const uint64_t bm = __ballot(sel);
+    for (int m = 0; m < EPR; ++m) {
+        const bool sel = u + 16 * m < c && (key[m] & pmask) >= prefix;
+        const uint32_t bits = row_bits16(__ballot(sel));
         if (sel) {
-            const int pos = base + __popcll(bm & lt);
-            sm.score[r][pos] = sv[m];
-            sm.idx[r][pos] = iv[m];
-            const uint32_t o = uint32_t(key[m] >> 32);
-            minord = o < minord ? o : minord;
+            pool[base + __popc(bits & lt)] = key_entry(key[m]);
+            kmin_sel = key[m] < kmin_sel ? key[m] : kmin_sel;
         }
-        base += __popcll(bm);
+        base += __popc(bits);
     }
-    minord = wave_min_u32(minord);
-    if (lane == 0) {
-        sm.cnt[r] = base;
-        sm.kept[r] = base;
-        sm.thr[r] = (base >= K) ? unord_f32(minord) - sm.eps[r] : -__builtin_inff();
+    kmin_sel = row_min16_u64(kmin_sel);
+    if (u == 0) {
+        cnt = base;
+        thr = base >= K ? key_entry(kmin_sel).s - eps : -__builtin_inff();
     }
-    __syncthreads();
+    return base;
 }
 
-// Sort row r's kept entries into canonical order and write them (plus pads). `row` is the
-// query position t within its batch; out_idx / out_scores point at that batch's (T, k_eff).
-template <int KP2, int RP, int POOL>
-__device__ void emit_row(TopkSmem<RP, POOL>& sm, int r, int64_t row, int64_t T, int64_t k_eff,
-                         int32_t* out_idx, float* out_scores)
+// Sort row r's (exactly scored) winners into canonical order and write them plus pads.
+// `row` is the query position t in its batch; out_idx/out_scores point at the batch.
+template <int KP2, int POOL>
+__device__ void emit_row(const Entry (&pool)[POOL], int kept, int64_t row, int64_t T,
+                         int64_t k_eff, int32_t* out_idx, float* out_scores, int u)
 {
-    constexpr int E2 = KP2 / 64;
-    const int lane = lane_id();
-    const int kept = sm.kept[r];
-    uint64_t key[E2];
+    constexpr int EPL = KP2 / 16;   // elements per lane; element i = u * EPL + m
+    uint64_t key[EPL];
 #pragma unroll
-    for (int m = 0; m < E2; ++m) {
-        const int i = 64 * m + lane;
-        key[m] = i < kept ? make_key(sm.score[r][i], sm.idx[r][i]) : 0ull;
+    for (int m = 0; m < EPL; ++m) {
+        const int i = u * EPL + m;
+        key[m] = i < kept ? make_key(pool[i].s, pool[i].j) : 0ull;
     }
-    // bitonic sort, descending
 #pragma unroll
     for (int kk = 2; kk <= KP2; kk <<= 1) {
 #pragma unroll
         for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-            if (jj >= 64) {
-                const int mj = jj >> 6;
+            if (jj < EPL) {
 #pragma unroll
-                for (int m = 0; m < E2; ++m) {
-                    if (m & mj) continue;
-                    const int m2 = m | mj;
-                    const int i = 64 * m + lane;
-                    const bool desc = (i & kk) == 0;
+                for (int m = 0; m < EPL; ++m) {
+                    if (m & jj) continue;
+                    const int m2 = m | jj;
+                    const bool desc = ((u * EPL + m) & kk) == 0;
                     const uint64_t a = key[m], b = key[m2];
                     const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
                     key[m] = desc ? hi : lo;
                     key[m2] = desc ? lo : hi;
                 }
             } else {
+                const int lx = jj / EPL;
 #pragma unroll
-                for (int m = 0; m < E2; ++m) {
-                    const int i = 64 * m + lane;
-                    const uint64_t other = shfl_xor_u64(key[m], jj);
-                    const bool low = (lane & jj) == 0;
+                for (int m = 0; m < EPL; ++m) {
+                    const int i = u * EPL + m;
+                    const uint64_t other = shfl_xor_u64(key[m], lx, 16);
+                    const bool low = (i & jj) == 0;
                     const bool desc = (i & kk) == 0;
                     const uint64_t hi = key[m] > other ? key[m] : other;
                     const uint64_t lo = key[m] > other ? other : key[m];
@@ -299,8 +415,8 @@ __device__ void emit_row(TopkSmem<RP, POOL>& sm, int r, int64_t row, int64_t T, 
     int32_t* oi = out_idx + row * k_eff;
     float* os = out_scores ? out_scores + row * k_eff : nullptr;
 #pragma unroll
-    for (int m = 0; m < E2; ++m) {
-        const int64_t i = 64 * m + lane;
+    for (int m = 0; m < EPL; ++m) {
+        const int64_t i = u * EPL + m;
         if (i >= k_eff) continue;
         if (i < kept) {
             oi[i] = int32_t(0xffffffffu - uint32_t(key[m]));
@@ -313,38 +429,54 @@ __device__ void emit_row(TopkSmem<RP, POOL>& sm, int r, int64_t row, int64_t T, 
 }
 
 // ------------------------------------------------------------------ kernels
-template <typename DT>
-__global__ __launch_bounds__(256) void key_absmax_kernel(TopkParams p)
+// Bound on |key element| per chunk of kAbsmaxChunk keys (one thread per key).
+template <typename DT, bool VEC>
+__global__ __launch_bounds__(kAbsmaxChunk) void key_absmax_kernel(TopkParams p)
 {
     const int64_t b = blockIdx.y;
-    const int64_t j0 = int64_t(blockIdx.x) * kAbsmaxChunk;
-    const int64_t j1 = min(p.T, j0 + kAbsmaxChunk);
-    const int64_t n = (j1 - j0) * p.R;
+    const int64_t jk = int64_t(blockIdx.x) * kAbsmaxChunk + threadIdx.x;
     const DT* kb = static_cast<const DT*>(p.key) + b * p.ksb;
+    const int R = int(p.R);
     float m = 0.0f;
-    for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
-        const int64_t j = j0 + e / p.R, d = e % p.R;
-        m = fmaxf(m, fabsf(to_f32(kb[j * p.kst + d * p.ksr])));
+    if (jk < p.T) {
+        for (int d0 = 0; d0 < R; d0 += 8) {
+            uint4 lo, hi;
+            load8<DT, VEC>(kb + jk * p.kst, p.ksr, d0, R, lo, hi);
+            float f[8];
+            to_f32x8<DT>(lo, hi, f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(f[e]));
+        }
     }
     m = wave_max(m);
-    __shared__ float part[4];
+    __shared__ float part[kAbsmaxChunk / 64];
     if (lane_id() == 0) part[threadIdx.x >> 6] = m;
     __syncthreads();
-    if (threadIdx.x == 0)
-        p.chunk_absmax[b * p.n_chunks + blockIdx.x] =
-            fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    if (threadIdx.x == 0) {
+        float r = part[0];
+        for (int i = 1; i < kAbsmaxChunk / 64; ++i) r = fmaxf(r, part[i]);
+        p.chunk_absmax[b * p.n_chunks + blockIdx.x] = r;
+    }
 }
 
 template <typename DT, bool VEC, int RC, int KP2>
-__global__ __launch_bounds__(64) void causal_topk_kernel(TopkParams p)
+__global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 {
     constexpr int RP = RC * 32;
-    constexpr int POOL = KP2 + 128;
+    constexpr int POOL = KP2 + 256;
+    constexpr int LIMIT = POOL - 16 * kWaves;   // a step appends <= 16 per row per wave
+    constexpr int HEADROOM = 64;                 // a prune must leave this much room
     __shared__ TopkSmem<RP, POOL> sm;
 
-    const int lane = threadIdx.x;
-    const int n = lane & 15;       // query row of this lane (MFMA column)
-    const int g = lane >> 4;       // lane group: dims 8g..8g+7 of each chunk, keys 4g..4g+3
+    const int lane = lane_id();
+    const int w = threadIdx.x >> 6;
+    // screening layout: MFMA column n = query row, lane group g = dims 8g..8g+7 / keys 4g..4g+3
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    // row-parallel layout: row rr owned by the 16 lanes u = 0..15 of DPP row (lane >> 4)
+    const int rr = 4 * w + (lane >> 4);
+    const int u = lane & 15;
+
     const int64_t T = p.T;
     const int64_t b = blockIdx.x % p.B;
     const int64_t rb = p.n_row_blocks - 1 - blockIdx.x / p.B;   // longest prefixes first
@@ -357,103 +489,123 @@ __global__ __launch_bounds__(64) void causal_topk_kernel(TopkParams p)
     const DT* qb = static_cast<const DT*>(p.query) + b * p.qsb;
     const DT* kb = static_cast<const DT*>(p.key) + b * p.ksb;
 
-    // query operands (B of the MFMA) and fp32 query rows in LDS
+    // query operands (B of the MFMA) in every wave; fp32 rows in LDS from wave 0
     uint4 qlo[RC], qhi[RC];
     const DT* qrow = qb + (row_ok ? row : 0) * p.qst;
 #pragma unroll
     for (int c = 0; c < RC; ++c) {
         load8<DT, VEC>(qrow, p.qsr, 32 * c + 8 * g, R, qlo[c], qhi[c]);
         if (!row_ok) { qlo[c] = make_uint4(0, 0, 0, 0); qhi[c] = qlo[c]; }
-        float f[8];
-        to_f32x8<DT>(qlo[c], qhi[c], f);
+        if (w == 0) {
+            float f[8];
+            to_f32x8<DT>(qlo[c], qhi[c], f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sm.q[n][32 * c + 8 * g + e] = f[e];
+            for (int e = 0; e < 8; ++e) sm.q[n][32 * c + 8 * g + e] = f[e];
+        }
     }
-    if (lane < kRows) {
-        sm.cnt[lane] = 0;
-        sm.kept[lane] = 0;
-        sm.thr[lane] = -__builtin_inff();
+    if (threadIdx.x < kRows) {
+        sm.cnt[threadIdx.x] = 0;
+        sm.thr[threadIdx.x] = -__builtin_inff();
     }
-    // bound on |key element| over the scanned prefix [0, last]
     float mk = 0.0f;
     const int64_t nch = last / kAbsmaxChunk + 1;
     for (int64_t c = lane; c < nch; c += 64) mk = fmaxf(mk, p.chunk_absmax[b * p.n_chunks + c]);
     mk = wave_max(mk);
     __syncthreads();
-    if (lane < kRows) {
+    if (threadIdx.x < kRows) {
         float l1 = 0.0f;
-        for (int d = 0; d < RP; ++d) l1 += fabsf(sm.q[lane][d]);
-        sm.eps[lane] = kEpsRel * (l1 * 1.0001f) * (mk + kTiny) + kTiny;
+        for (int d = 0; d < RP; ++d) l1 += fabsf(sm.q[threadIdx.x][d]);
+        sm.eps[threadIdx.x] = kEpsRel * (l1 * 1.0001f) * (mk + kTiny) + kTiny;
     }
     __syncthreads();
 
+    // ---- screen
     float th = -__builtin_inff();
     const int64_t nsteps = last / 16 + 1;
+    const int64_t iters = (nsteps + kWaves - 1) / kWaves;
     uint4 plo[kPrefetch][RC], phi[kPrefetch][RC];
 #pragma unroll
-    for (int u = 0; u < kPrefetch; ++u) {
-        const int64_t j = min(int64_t(u) * 16 + n, T - 1);
+    for (int v = 0; v < kPrefetch; ++v) {
+        const int64_t st = w + int64_t(kWaves) * v;
+        const int64_t j = min(st * 16 + n, T - 1);
 #pragma unroll
-        for (int c = 0; c < RC; ++c) load8<DT, VEC>(kb + j * p.kst, p.ksr, 32 * c + 8 * g, R, plo[u][c], phi[u][c]);
+        for (int c = 0; c < RC; ++c) {
+            plo[v][c] = make_uint4(0, 0, 0, 0);
+            phi[v][c] = plo[v][c];
+            if (st < nsteps) load8<DT, VEC>(kb + j * p.kst, p.ksr, 32 * c + 8 * g, R, plo[v][c], phi[v][c]);
+        }
     }
-
-    for (int64_t s0 = 0; s0 < nsteps; s0 += kPrefetch) {
+    for (int64_t it0 = 0; it0 < iters; it0 += kPrefetch) {
 #pragma unroll
-        for (int u = 0; u < kPrefetch; ++u) {
-            const int64_t st = s0 + u;
-            if (st >= nsteps) break;
-            uint4 alo[RC], ahi[RC];
+        for (int v = 0; v < kPrefetch; ++v) {
+            const int64_t it = it0 + v;
+            if (it >= iters) break;
+            const int64_t st = w + int64_t(kWaves) * it;
+            if (st < nsteps) {
+                uint4 alo[RC], ahi[RC];
 #pragma unroll
-            for (int c = 0; c < RC; ++c) { alo[c] = plo[u][c]; ahi[c] = phi[u][c]; }
-            {   // refill this slot with step st + kPrefetch
-                const int64_t j = min((st + kPrefetch) * 16 + n, T - 1);
-                if (st + kPrefetch < nsteps) {
+                for (int c = 0; c < RC; ++c) { alo[c] = plo[v][c]; ahi[c] = phi[v][c]; }
+                const int64_t stn = st + int64_t(kWaves) * kPrefetch;
+                if (stn < nsteps) {
+                    const int64_t j = min(stn * 16 + n, T - 1);
 #pragma unroll
                     for (int c = 0; c < RC; ++c)
-                        load8<DT, VEC>(kb + j * p.kst, p.ksr, 32 * c + 8 * g, R, plo[u][c], phi[u][c]);
+                        load8<DT, VEC>(kb + j * p.kst, p.ksr, 32 * c + 8 * g, R, plo[v][c], phi[v][c]);
+                }
+                f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int c = 0; c < RC; ++c) acc = mfma_chunk<DT>(alo[c], ahi[c], qlo[c], qhi[c], acc);
+                const int64_t j0 = st * 16;
+                const bool diag = (j0 == r0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t j = j0 + 4 * g + i;
+                    if (row_ok && acc[i] >= th && (!diag || j <= row)) {
+                        const int pos = atomicAdd(&sm.cnt[n], 1);
+                        sm.pool[n][pos] = Entry{acc[i], uint32_t(j)};
+                    }
                 }
             }
-            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int c = 0; c < RC; ++c) acc = mfma_chunk<DT>(alo[c], ahi[c], qlo[c], qhi[c], acc);
-
-            const int64_t j0 = st * 16;
-            const bool diag = (j0 == r0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t j = j0 + 4 * g + i;
-                const bool pass = row_ok && acc[i] >= th && (!diag || j <= row);
-                if (pass) {
-                    const int pos = atomicAdd(&sm.cnt[n], 1);
-                    sm.idx[n][pos] = uint32_t(j);
+            __syncthreads();
+            const bool over = lane < kRows && sm.cnt[lane] > LIMIT;
+            if (__ballot(over)) {   // same decision in every wave: all read after the barrier
+                const int c = sm.cnt[rr];
+                if (c > K) {
+                    int c2 = c;
+                    const bool ok = prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr],
+                                                    sm.thr[rr], sm.eps[rr], K, u);
+                    if (!ok || c2 > LIMIT - HEADROOM)
+                        exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c2, sm.cnt[rr],
+                                                     sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
+                                                     p.ksr, R, K, u);
                 }
-            }
-            const int c = sm.cnt[n];
-            uint64_t full = __ballot(lane < kRows && c > POOL - 16);
-            if (full) {
-                while (full) {
-                    const int r = __ffsll((unsigned long long)full) - 1;
-                    full &= full - 1;
-                    compact_row<DT, VEC, RP, POOL>(sm, r, K, kb, p.kst, p.ksr, R);
-                }
+                __syncthreads();
                 th = sm.thr[n];
             }
         }
     }
 
-    // finish every row: rescore what is pending, select, sort, write
-    for (int r = 0; r < kRows; ++r) {
-        if (r0 + r >= T) break;
-        compact_row<DT, VEC, RP, POOL>(sm, r, K, kb, p.kst, p.ksr, R);
-        emit_row<KP2, RP, POOL>(sm, r, r0 + r, T, p.k_eff, p.out_idx + b * T * p.k_eff,
-                                p.out_scores ? p.out_scores + b * T * p.k_eff : nullptr);
+    // ---- finish: prune, rescore exactly, select, sort, write
+    __syncthreads();
+    if (r0 + rr < T) {
+        int c = sm.cnt[rr];
+        if (c > K) {
+            int c2 = c;
+            prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
+            c = c2;
+        }
+        const int kept = exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c, sm.cnt[rr],
+                                                      sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
+                                                      p.ksr, R, K, u);
+        emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, p.out_idx + b * T * p.k_eff,
+                            p.out_scores ? p.out_scores + b * T * p.k_eff : nullptr, u);
     }
 }
 
 template <typename DT, bool VEC, int RC>
 hipError_t launch_topk_k(const TopkParams& p, hipStream_t s)
 {
-    const dim3 grid(unsigned(p.B * p.n_row_blocks)), block(64);
+    const dim3 grid(unsigned(p.B * p.n_row_blocks)), block(64 * kWaves);
     if (p.k_eff <= 64) causal_topk_kernel<DT, VEC, RC, 64><<<grid, block, 0, s>>>(p);
     else if (p.k_eff <= 128) causal_topk_kernel<DT, VEC, RC, 128><<<grid, block, 0, s>>>(p);
     else causal_topk_kernel<DT, VEC, RC, 256><<<grid, block, 0, s>>>(p);
@@ -474,15 +626,22 @@ hipError_t launch_topk_t(bool vec, const TopkParams& p, hipStream_t s)
     return vec ? launch_topk_r<DT, true>(p, s) : launch_topk_r<DT, false>(p, s);
 }
 
+template <typename DT>
+hipError_t launch_absmax_t(bool vec, const TopkParams& p, hipStream_t s)
+{
+    const dim3 grid(unsigned(p.n_chunks), unsigned(p.B)), block(kAbsmaxChunk);
+    if (vec) key_absmax_kernel<DT, true><<<grid, block, 0, s>>>(p);
+    else key_absmax_kernel<DT, false><<<grid, block, 0, s>>>(p);
+    return hipGetLastError();
+}
+
 }  // namespace
 
-hipError_t launch_key_absmax(int dtype, const TopkParams& p, hipStream_t s)
+hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s)
 {
-    const dim3 grid(unsigned(p.n_chunks), unsigned(p.B)), block(256);
-    if (dtype == 2) key_absmax_kernel<bf16_t><<<grid, block, 0, s>>>(p);
-    else if (dtype == 1) key_absmax_kernel<_Float16><<<grid, block, 0, s>>>(p);
-    else key_absmax_kernel<float><<<grid, block, 0, s>>>(p);
-    return hipGetLastError();
+    if (dtype == 2) return launch_absmax_t<bf16_t>(vec, p, s);
+    if (dtype == 1) return launch_absmax_t<_Float16>(vec, p, s);
+    return launch_absmax_t<float>(vec, p, s);
 }
 
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s)
