@@ -148,6 +148,29 @@ def _cpu_model():
     return "unknown"
 
 
+def run_leg(args, dev, K, scale, readout_bytes):
+    """One kernel (or a plain copy) in isolation, for rocprofv3 counter passes."""
+    from routing_attention.kernels import causal_topk, sparse_meat_attention
+
+    if args.leg == "copy":
+        src = torch.empty(128 * 2 ** 20, dtype=torch.bfloat16, device=dev["q"].device).normal_()
+        dst = torch.empty_like(src)
+        ms = time_loop(lambda: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"leg": "copy", "bytes_read": src.numel() * 2,
+                          "bytes_written": dst.numel() * 2, "ms": round(ms, 4)}), flush=True)
+        return
+    if args.leg == "topk":
+        fn = lambda: causal_topk(dev["qa"], dev["ka"], K)  # noqa: E731
+        ms = time_loop(fn, args.steps, args.warmup)
+        print(json.dumps({"leg": "topk", "ms": round(ms, 4)}), flush=True)
+        return
+    idx = causal_topk(dev["qa"], dev["ka"], K)
+    fn = lambda: sparse_meat_attention(dev["q"], dev["k"], dev["v"], idx, scale)  # noqa: E731
+    ms = time_loop(fn, args.steps, args.warmup)
+    print(json.dumps({"leg": "readout", "ms": round(ms, 4),
+                      "algorithmic_gbs": round(readout_bytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,6 +179,9 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
+    ap.add_argument("--leg", default="all", choices=["all", "topk", "readout", "copy"],
+                    help="profiling aid: run only one kernel (or a 256 MiB device copy used to "
+                         "calibrate the FETCH_SIZE / WRITE_SIZE counters) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this path has no multi-GPU code "
@@ -174,6 +200,10 @@ def main():
 
     def step():
         return fused_sparse_attention(dev["qa"], dev["ka"], dev["q"], dev["k"], dev["v"], K, scale)
+
+    if args.leg != "all":
+        run_leg(args, dev, K, scale, readout_bytes)
+        return
 
     torch.cuda.reset_peak_memory_stats()
     base_mem = torch.cuda.memory_allocated()

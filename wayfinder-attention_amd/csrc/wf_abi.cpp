@@ -151,12 +151,19 @@ int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t 
     p.seg_per_pair = 8 / gcd64(nbh, 8);
     p.rows_per_seg = cdiv(T, p.seg_per_pair);
     p.vpairs = nbh * p.seg_per_pair;
-    p.wg_per_vpair = cdiv(p.rows_per_seg, 4);
+    p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
     const int64_t grid = p.vpairs * p.wg_per_vpair;
     if (grid >= (int64_t(1) << 31)) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: problem too large for one launch");
     const bool vec = vec_ok(q, dtype, qs, 4, D) && vec_ok(k, dtype, ks, 4, D) &&
                      vec_ok(v, dtype, vs, 4, D) && vec_ok(out, dtype, os, 4, D);
-    const hipError_t e = wf::launch_sparse_readout(dtype, vec, p, stream);
+    // fast path: 32-bit byte offsets cover each (b, h) span of q/k/v/out, contiguous index
+    // rows, non-negative row strides
+    const int64_t es = int64_t(elem_size(dtype));
+    auto span_ok = [&](const int64_t* st) {
+        return st[2] >= 0 && (T - 1) * st[2] * es + D * es < (int64_t(1) << 32);
+    };
+    const bool fast = vec && is[2] == 1 && span_ok(qs) && span_ok(ks) && span_ok(vs) && span_ok(os);
+    const hipError_t e = wf::launch_sparse_readout(dtype, vec, fast, p, stream);
     if (e != hipSuccess) return hip_fail("sparse_readout: kernel launch", e);
     return WF_OK;
 }

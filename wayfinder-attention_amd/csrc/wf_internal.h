@@ -128,10 +128,12 @@ struct ReadoutParams {
 
 // Key-magnitude chunk size of the screening bound (keys per chunk).
 constexpr int kAbsmaxChunk = 256;
+// Query rows per readout workgroup (4 waves x 4 consecutive rows).
+constexpr int kReadoutRowsPerWG = 16;
 
 // launchers (return hipError_t of the launch)
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s);
-hipError_t launch_sparse_readout(int dtype, bool vec, const ReadoutParams& p, hipStream_t s);
+hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutParams& p, hipStream_t s);
 
 }  // namespace wf

@@ -5,12 +5,13 @@
 // (B, H, T, K, D) tensors (2 GiB each at T=16384, H=8, K=128, bf16) and runs two batched
 // GEMVs; here every gathered K/V row goes straight from memory to registers:
 //
-//  - one wave per (b, h, t) query row; D/8 lanes share one neighbour (8 dims, one 16-byte
-//    load each), so a wave step covers 64*8/D neighbours with full 128-byte lines;
-//  - all K and V rows of a batch of steps are loaded before any is used (up to 32 KiB in
-//    flight per wave), scores reduce over the D/8 lanes of a neighbour with xor shuffles,
-//    and an online softmax (exp2 with log2(e) folded into the scale) carries max and sum
-//    across batches; fp32 accumulation, one rounding to the output dtype;
+//  - a wave walks 4 consecutive (b, h, t) query rows; D/8 lanes share one neighbour (8 dims,
+//    one 16-byte load each), so a wave step covers 64*8/D neighbours with full 128-byte
+//    lines. The rows are cut into tasks of 4 steps and software-pipelined: indices are
+//    fetched two tasks ahead and the K/V rows one task ahead of the compute;
+//  - q.k uses v_dot2_f32_{bf16,f16} (fp32 FMA for fp32 inputs) and a DPP reduction over the
+//    D/8 lanes of a neighbour; an online softmax (exp2, log2(e) folded into the scale)
+//    carries max and sum across tasks; fp32 accumulation, one rounding to the output;
 //  - workgroups are mapped so that all rows of one (b, h) pair run on one XCD: blockIdx
 //    modulo 8 picks the XCD under round-robin dispatch, which keeps that head's K and V
 //    (2 x T x D x s bytes, 4 MiB at the benchmark shape) in that XCD's 4 MiB L2.
@@ -19,7 +20,8 @@
 namespace wf {
 namespace {
 
-constexpr int kWaves = 4;        // waves (rows) per workgroup
+constexpr int kWaves = 4;        // waves per workgroup
+constexpr int kRowsPerWave = kReadoutRowsPerWG / kWaves;  // consecutive query rows per wave
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename DT, bool VEC>
@@ -79,16 +81,86 @@ __device__ __forceinline__ void store_row8(DT* p, int64_t sd, const float* f)
     }
 }
 
-// D: head dim (32, 64, 128). NB: wave steps whose loads are issued together.
+// ---------------------------------------------------------------- reductions
+// Sum over the LPN lanes that share one neighbour (LPN in {4, 8, 16}), with DPP moves:
+// quad_perm xor 1 and xor 2 sum each quad; row_half_mirror then adds the other quad of the
+// 8-lane group and row_mirror the other half of the 16-lane row.
+template <int LPN>
+__device__ __forceinline__ float group_sum(float x)
+{
+    x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xf, 0xf, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xf, 0xf, false));
+    if constexpr (LPN >= 8)
+        x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xf, 0xf, false));
+    if constexpr (LPN >= 16)
+        x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xf, 0xf, false));
+    return x;
+}
+
+// Reduce over the 64/LPN neighbour groups of the wave (lanes that differ in bits >= LPN).
+template <int LPN, bool MAX>
+__device__ __forceinline__ float across_groups(float x)
+{
+#pragma unroll
+    for (int o = LPN; o < 64; o <<= 1) {
+        const float y = __shfl_xor(x, o, 64);
+        x = MAX ? fmaxf(x, y) : x + y;
+    }
+    return x;
+}
+
+// Dot product of 8 query dims with 8 key dims (raw 16-byte words; fp32 uses lo and hi).
+template <typename DT>
+__device__ __forceinline__ float dot8(const uint4& qlo, const uint4& qhi, const uint4& klo,
+                                      const uint4& khi)
+{
+    if constexpr (__is_same(DT, bf16_t)) {
+        typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 v2;
+        float d = 0.0f;
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, qlo.x), __builtin_bit_cast(v2, klo.x), d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, qlo.y), __builtin_bit_cast(v2, klo.y), d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, qlo.z), __builtin_bit_cast(v2, klo.z), d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, qlo.w), __builtin_bit_cast(v2, klo.w), d, false);
+        return d;
+    } else if constexpr (__is_same(DT, _Float16)) {
+        typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 v2;
+        float d = 0.0f;
+        d = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, qlo.x), __builtin_bit_cast(v2, klo.x), d, false);
+        d = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, qlo.y), __builtin_bit_cast(v2, klo.y), d, false);
+        d = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, qlo.z), __builtin_bit_cast(v2, klo.z), d, false);
+        d = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, qlo.w), __builtin_bit_cast(v2, klo.w), d, false);
+        return d;
+    } else {
+        float q[8], k[8];
+        cvt8<float>(qlo, qhi, q);
+        cvt8<float>(klo, khi, k);
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(q[e], k[e], d);
+        return d;
+    }
+}
+
+// One task = NB wave steps of one query row (NB * 64/LPN neighbour slots). The stage holds
+// what a task needs before its compute: key indices, validity, the query slice.
+template <int NB>
+struct Stage {
+    int j[NB];
+    bool ok[NB];
+    uint4 qlo, qhi;
+};
+
+// D: head dim (32, 64, 128); NB: wave steps per task.
 template <typename DT, bool VEC, int D, int NB>
 __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutParams p)
 {
-    constexpr int LPN = D / 8;      // lanes per neighbour
-    constexpr int NPS = 64 / LPN;   // neighbours per wave step
+    constexpr int LPN = D / 8;       // lanes per neighbour
+    constexpr int NPS = 64 / LPN;    // neighbours per wave step
+    constexpr int CH = NB * NPS;     // neighbour slots per task
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int sub = lane % LPN;     // 8-dim slice of the head
-    const int grp = lane / LPN;     // neighbour within a step
+    const int sub = lane % LPN;      // 8-dim slice of the head
+    const int grp = lane / LPN;      // neighbour within a step
 
     // XCD-aware mapping: blockIdx % 8 is the XCD; virtual pair vp runs on XCD vp % 8.
     const int64_t xcd = blockIdx.x & 7;
@@ -101,61 +173,71 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
     const int64_t b = pair / p.H, h = pair % p.H;
     const int64_t t0 = seg * p.rows_per_seg;
     const int64_t t1 = min(p.T, t0 + p.rows_per_seg);
-    const int64_t t = t0 + chunk * kWaves + wave;
-    if (t >= t1) return;
+    const int64_t tw = t0 + (chunk * kWaves + wave) * kRowsPerWave;   // first row of this wave
+    if (tw >= t1) return;
+    const int nrows = int(min(int64_t(kRowsPerWave), t1 - tw));
 
     const int64_t T = p.T;
     const int K = int(p.K);
-    const bool mask_pads = (p.flags & 1u) && t < K - 1;
+    const int nb = (K + CH - 1) / CH;
+    const int ntask = nrows * nb;
+    const bool mask_flag = (p.flags & 1u) != 0;
+    const float sl2 = p.scale * kLog2e;   // scale multiplies the finished dot, as in the reference
 
-    const DT* qp = static_cast<const DT*>(p.q) + b * p.qs[0] + h * p.qs[1] + t * p.qs[2] + int64_t(sub) * 8 * p.qs[3];
+    const DT* qbase = static_cast<const DT*>(p.q) + b * p.qs[0] + h * p.qs[1] + int64_t(sub) * 8 * p.qs[3];
     const DT* kbase = static_cast<const DT*>(p.k) + b * p.ks[0] + h * p.ks[1] + int64_t(sub) * 8 * p.ks[3];
     const DT* vbase = static_cast<const DT*>(p.v) + b * p.vs[0] + h * p.vs[1] + int64_t(sub) * 8 * p.vs[3];
-    const int32_t* ip = p.idx + b * p.is[0] + t * p.is[1];
+    const int32_t* ibase = p.idx + b * p.is[0];
 
-    float qf[8];
-    {
-        uint4 lo, hi;
-        load_row8<DT, VEC>(qp, p.qs[3], lo, hi);
-        cvt8<DT>(lo, hi, qf);
-    }
-    // the scale multiplies the finished dot product, as in the reference; log2(e) rides
-    // along so the softmax can use exp2
-    const float sl2 = p.scale * kLog2e;
-
-    float m = -__builtin_inff();   // running max (log2 domain), wave-uniform
-    float l = 0.0f;                // this lane group's share of the softmax denominator
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-
-    for (int s0 = 0; s0 < K; s0 += NB * NPS) {
-        uint4 klo[NB], khi[NB], vlo[NB], vhi[NB];
-        bool ok[NB];
+    auto fetch_idx = [&](int tau, Stage<NB>& st) {
+        const int64_t t = tw + tau / nb;
+        const int bat = tau % nb;
+        const int32_t* ip = ibase + t * p.is[1];
+        const bool mp = mask_flag && t < K - 1;
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            const int slot = s0 + u * NPS + grp;
-            ok[u] = slot < K && !(mask_pads && slot > t);
-            int64_t j = slot < K ? int64_t(ip[int64_t(slot) * p.is[2]]) : 0;
+            const int slot = bat * CH + u * NPS + grp;
+            const bool in = slot < K;
+            st.ok[u] = in && !(mp && slot > t);
+            int64_t j = in ? int64_t(ip[int64_t(slot) * p.is[2]]) : 0;
             if (j < 0) j += T;
-            j = j < 0 ? 0 : (j > T - 1 ? T - 1 : j);
-            load_row8<DT, VEC>(kbase + j * p.ks[2], p.ks[3], klo[u], khi[u]);
-            load_row8<DT, VEC>(vbase + j * p.vs[2], p.vs[3], vlo[u], vhi[u]);
+            st.j[u] = int(j < 0 ? 0 : (j > T - 1 ? T - 1 : j));
+        }
+        if (bat == 0) load_row8<DT, VEC>(qbase + t * p.qs[2], p.qs[3], st.qlo, st.qhi);
+    };
+    auto fetch_kv = [&](const Stage<NB>& st, uint4 (&klo)[NB], uint4 (&khi)[NB], uint4 (&vlo)[NB],
+                        uint4 (&vhi)[NB]) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            load_row8<DT, VEC>(kbase + int64_t(st.j[u]) * p.ks[2], p.ks[3], klo[u], khi[u]);
+            load_row8<DT, VEC>(vbase + int64_t(st.j[u]) * p.vs[2], p.vs[3], vlo[u], vhi[u]);
+        }
+    };
+
+    uint4 qlo = make_uint4(0, 0, 0, 0), qhi = qlo;
+    float m = -__builtin_inff(), l = 0.0f;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+
+    auto compute = [&](int tau, const Stage<NB>& st, const uint4 (&klo)[NB], const uint4 (&khi)[NB],
+                       const uint4 (&vlo)[NB], const uint4 (&vhi)[NB]) {
+        const int bat = tau % nb;
+        if (bat == 0) {
+            qlo = st.qlo;
+            qhi = st.qhi;
+            m = -__builtin_inff();
+            l = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
         }
         float sc[NB];
         float bm = -__builtin_inff();
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            float kf[8];
-            cvt8<DT>(klo[u], khi[u], kf);
-            float d = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) d = fmaf(qf[e], kf[e], d);
-#pragma unroll
-            for (int o = 1; o < LPN; o <<= 1) d += __shfl_xor(d, o, 64);
-            sc[u] = ok[u] ? d * sl2 : -__builtin_inff();
+            const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
+            sc[u] = st.ok[u] ? d * sl2 : -__builtin_inff();
             bm = fmaxf(bm, sc[u]);
         }
-#pragma unroll
-        for (int o = LPN; o < 64; o <<= 1) bm = fmaxf(bm, __shfl_xor(bm, o, 64));
+        bm = across_groups<LPN, true>(bm);
         const float mn = fmaxf(m, bm);
         const float alpha = (mn == -__builtin_inff()) ? 1.0f : exp2f(m - mn);
         l *= alpha;
@@ -163,7 +245,7 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
         for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            const float pu = ok[u] ? exp2f(sc[u] - mn) : 0.0f;
+            const float pu = st.ok[u] ? exp2f(sc[u] - mn) : 0.0f;
             l += pu;
             float vf[8];
             cvt8<DT>(vlo[u], vhi[u], vf);
@@ -171,29 +253,297 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
             for (int e = 0; e < 8; ++e) acc[e] = fmaf(pu, vf[e], acc[e]);
         }
         m = mn;
-    }
-    // combine the lane groups (different neighbours, same dims)
+        if (bat == nb - 1) {
+            // combine the lane groups (different neighbours, same dims) and store the row
+            const float lt = across_groups<LPN, false>(l);
+            float o8[8];
 #pragma unroll
-    for (int o = LPN; o < 64; o <<= 1) {
-        l += __shfl_xor(l, o, 64);
+            for (int e = 0; e < 8; ++e) o8[e] = across_groups<LPN, false>(acc[e]);
+            if (grp == 0) {
+                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+                for (int e = 0; e < 8; ++e) o8[e] *= inv;
+                const int64_t t = tw + tau / nb;
+                DT* op = static_cast<DT*>(p.out) + b * p.os[0] + h * p.os[1] + t * p.os[2] + int64_t(sub) * 8 * p.os[3];
+                store_row8<DT, VEC>(op, p.os[3], o8);
+            }
+        }
+    };
+
+    // two-deep software pipeline: indices two tasks ahead, K/V one task ahead
+    Stage<NB> sA, sB;
+    uint4 kAlo[NB], kAhi[NB], vAlo[NB], vAhi[NB], kBlo[NB], kBhi[NB], vBlo[NB], vBhi[NB];
+    fetch_idx(0, sA);
+    fetch_kv(sA, kAlo, kAhi, vAlo, vAhi);
+    if (ntask > 1) fetch_idx(1, sB);
+    for (int tau = 0; tau < ntask; tau += 2) {
+        if (tau + 1 < ntask) fetch_kv(sB, kBlo, kBhi, vBlo, vBhi);
+        const Stage<NB> cA = sA;
+        if (tau + 2 < ntask) fetch_idx(tau + 2, sA);
+        compute(tau, cA, kAlo, kAhi, vAlo, vAhi);
+        if (tau + 1 < ntask) {
+            if (tau + 2 < ntask) fetch_kv(sA, kAlo, kAhi, vAlo, vAhi);
+            const Stage<NB> cB = sB;
+            if (tau + 3 < ntask) fetch_idx(tau + 3, sB);
+            compute(tau + 1, cB, kBlo, kBhi, vBlo, vBhi);
+        }
     }
-    if (grp == 0) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float o8[8];
+}
+
+// ---------------------------------------------------------------- fast path
+// Aligned (B,T,H,D)-style layouts whose per-(b,h) span fits 32-bit byte offsets: every
+// gather is a global load from a uniform 64-bit base plus a 32-bit per-lane offset. Each
+// lane group keeps its own online-softmax state (max, sum, 8 accumulators) across the
+// row's tasks; the groups are combined once per row (DPP row_ror within 16-lane rows, two
+// shuffles across rows), so the per-step work has no LDS or ds_bpermute traffic.
+
+template <int N>   // rotate right by N lanes within each 16-lane row
+__device__ __forceinline__ float dpp_ror(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 + N, 0xf, 0xf, false));
+}
+
+// op over the lane groups of the wave (groups = lanes with equal bits below LPN): DPP
+// row_ror inside each 16-lane row, then xor-16 / xor-32 shuffles across rows. (The
+// gfx950 v_permlane{16,32}_swap builtins would avoid the shuffles, but this toolchain
+// folds their two results into one when both feed the same expression.)
+template <int LPN, bool MAX>
+__device__ __forceinline__ float group_allreduce(float x)
+{
+    if constexpr (LPN <= 4) { const float y = dpp_ror<4>(x); x = MAX ? fmaxf(x, y) : x + y; }
+    if constexpr (LPN <= 8) { const float y = dpp_ror<8>(x); x = MAX ? fmaxf(x, y) : x + y; }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o8[e] = acc[e] * inv;
-        DT* op = static_cast<DT*>(p.out) + b * p.os[0] + h * p.os[1] + t * p.os[2] + int64_t(sub) * 8 * p.os[3];
-        store_row8<DT, VEC>(op, p.os[3], o8);
+    for (int o = 16; o < 64; o <<= 1) {
+        const float y = __shfl_xor(x, o, 64);
+        x = MAX ? fmaxf(x, y) : x + y;
     }
+    return x;
+}
+
+template <typename DT>
+__device__ __forceinline__ void ld16(const char* base, uint32_t off, uint4& lo, uint4& hi)
+{
+    lo = *reinterpret_cast<const uint4*>(base + off);
+    if constexpr (sizeof(DT) == 4) hi = *reinterpret_cast<const uint4*>(base + off + 16u);
+    else hi = make_uint4(0, 0, 0, 0);
+}
+
+// acc[0..7] += pa * va[0..7] + pb * vb[0..7]  (two neighbours of one lane group)
+template <typename DT>
+__device__ __forceinline__ void pv2(float* acc, float pa, float pb, const uint4& valo, const uint4& vahi,
+                                    const uint4& vblo, const uint4& vbhi)
+{
+    if constexpr (__is_same(DT, bf16_t)) {
+        typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 v2;
+        const v2 pp = {(__bf16)pa, (__bf16)pb};
+        const uint32_t a[4] = {valo.x, valo.y, valo.z, valo.w};
+        const uint32_t b[4] = {vblo.x, vblo.y, vblo.z, vblo.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t lo = __builtin_amdgcn_perm(b[w], a[w], 0x05040100u);   // (a.lo, b.lo)
+            const uint32_t hi = __builtin_amdgcn_perm(b[w], a[w], 0x07060302u);   // (a.hi, b.hi)
+            acc[2 * w] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, lo), pp, acc[2 * w], false);
+            acc[2 * w + 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, hi), pp, acc[2 * w + 1], false);
+        }
+    } else if constexpr (__is_same(DT, _Float16)) {
+        typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 v2;
+        const v2 pp = {(_Float16)pa, (_Float16)pb};
+        const uint32_t a[4] = {valo.x, valo.y, valo.z, valo.w};
+        const uint32_t b[4] = {vblo.x, vblo.y, vblo.z, vblo.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t lo = __builtin_amdgcn_perm(b[w], a[w], 0x05040100u);
+            const uint32_t hi = __builtin_amdgcn_perm(b[w], a[w], 0x07060302u);
+            acc[2 * w] = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, lo), pp, acc[2 * w], false);
+            acc[2 * w + 1] = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, hi), pp, acc[2 * w + 1], false);
+        }
+    } else {
+        float fa[8], fb[8];
+        cvt8<float>(valo, vahi, fa);
+        cvt8<float>(vblo, vbhi, fb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(pb, fb[e], fmaf(pa, fa[e], acc[e]));
+    }
+}
+
+// NB (even): wave steps per task.
+template <typename DT, int D, int NB>
+__global__ __launch_bounds__(64 * kWaves) void sparse_readout_fast(ReadoutParams p)
+{
+    static_assert(NB % 2 == 0, "steps are consumed in pairs");
+    constexpr int LPN = D / 8;
+    constexpr int NPS = 64 / LPN;
+    constexpr int CH = NB * NPS;
+    constexpr uint32_t ES = sizeof(DT);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+    const int sub = lane % LPN;
+    const int grp = lane / LPN;
+
+    const int64_t xcd = blockIdx.x & 7;
+    const int64_t it = blockIdx.x >> 3;
+    const int64_t vp = (it / p.wg_per_vpair) * 8 + xcd;
+    if (vp >= p.vpairs) return;
+    const int64_t chunk = it % p.wg_per_vpair;
+    const int64_t pair = vp / p.seg_per_pair;
+    const int64_t seg = vp % p.seg_per_pair;
+    const int64_t b = pair / p.H, h = pair % p.H;
+    const int64_t t0 = seg * p.rows_per_seg;
+    const int64_t t1 = min(p.T, t0 + p.rows_per_seg);
+    const int64_t tw = t0 + (chunk * kWaves + wave) * kRowsPerWave;
+    if (tw >= t1) return;
+    const int nrows = int(min(int64_t(kRowsPerWave), t1 - tw));
+
+    const int K = int(p.K);
+    const int T = int(p.T);
+    const int nb = (K + CH - 1) / CH;
+    const bool mask_flag = (p.flags & 1u) != 0;
+    const float sl2 = p.scale * kLog2e;
+
+    const char* kb = reinterpret_cast<const char*>(static_cast<const DT*>(p.k) + b * p.ks[0] + h * p.ks[1]);
+    const char* vb = reinterpret_cast<const char*>(static_cast<const DT*>(p.v) + b * p.vs[0] + h * p.vs[1]);
+    const char* qb = reinterpret_cast<const char*>(static_cast<const DT*>(p.q) + b * p.qs[0] + h * p.qs[1] + tw * p.qs[2]);
+    char* ob = reinterpret_cast<char*>(static_cast<DT*>(p.out) + b * p.os[0] + h * p.os[1] + tw * p.os[2]);
+    const uint32_t krow = uint32_t(p.ks[2]) * ES, vrow = uint32_t(p.vs[2]) * ES;
+    const uint32_t qrow = uint32_t(p.qs[2]) * ES, orow = uint32_t(p.os[2]) * ES;
+    const uint32_t loff = uint32_t(sub) * 8u * ES;
+    const int32_t* ib = p.idx + b * p.is[0] + tw * p.is[1];
+    const int64_t irow = p.is[1];
+
+    // stage I: offsets (+ query slice at a row's first task) of the task whose K/V load is next
+    uint32_t ko[NB], vo[NB];
+    uint4 qIlo, qIhi;
+    int ri = 0, qi = 0;   // task of stage I
+    auto fetch_idx = [&]() {
+        const char* ip = reinterpret_cast<const char*>(ib + ri * irow);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int slot = min(qi * CH + u * NPS + grp, K - 1);
+            int j = *reinterpret_cast<const int*>(ip + uint32_t(slot) * 4u);
+            j += (j >> 31) & T;
+            j = min(max(j, 0), T - 1);
+            ko[u] = uint32_t(j) * krow + loff;
+            vo[u] = uint32_t(j) * vrow + loff;
+        }
+        if (qi == 0) ld16<DT>(qb, uint32_t(ri) * qrow + loff, qIlo, qIhi);
+    };
+    auto advance = [&](int& r, int& q) { if (++q == nb) { q = 0; ++r; } };
+
+    // compute state
+    uint4 qlo = make_uint4(0, 0, 0, 0), qhi = qlo;
+    float m = -__builtin_inff(), l = 0.0f;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int rc = 0, qc = 0;   // task being computed
+
+    auto compute = [&](const uint4 (&klo)[NB], const uint4 (&khi)[NB], const uint4 (&vlo)[NB],
+                       const uint4 (&vhi)[NB], const uint4& qnlo, const uint4& qnhi) {
+        if (qc == 0) {
+            qlo = qnlo;
+            qhi = qnhi;
+            m = -__builtin_inff();
+            l = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+        }
+        const int t = int(tw) + rc;
+        const int slot0 = qc * CH + grp;
+        const int lim = (mask_flag && t < K - 1) ? t + 1 : K;   // slots >= lim carry no weight
+        float sc[NB];
+        float bm = -__builtin_inff();
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
+            sc[u] = slot0 + u * NPS < lim ? d * sl2 : -__builtin_inff();
+            bm = fmaxf(bm, sc[u]);
+        }
+        const float mn = fmaxf(m, bm);
+        const float alpha = m == -__builtin_inff() ? 0.0f : exp2f(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+#pragma unroll
+        for (int u = 0; u < NB; u += 2) {
+            const float pa = sc[u] == -__builtin_inff() ? 0.0f : exp2f(sc[u] - mn);
+            const float pc = sc[u + 1] == -__builtin_inff() ? 0.0f : exp2f(sc[u + 1] - mn);
+            l += pa + pc;
+            pv2<DT>(acc, pa, pc, vlo[u], vhi[u], vlo[u + 1], vhi[u + 1]);
+        }
+        m = mn;
+        if (qc == nb - 1) {
+            const float mm = group_allreduce<LPN, true>(m);
+            const float f = m == -__builtin_inff() ? 0.0f : exp2f(m - mm);
+            const float lt = group_allreduce<LPN, false>(l * f);
+            float o8[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o8[e] = group_allreduce<LPN, false>(acc[e] * f);
+            if (grp == 0) {
+                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o8[e] *= inv;
+                store_row8<DT, true>(reinterpret_cast<DT*>(ob + uint32_t(rc) * orow + loff), 1, o8);
+            }
+        }
+        advance(rc, qc);
+    };
+
+    const int ntask = nrows * nb;
+    uint4 qAlo, qAhi, qBlo, qBhi;
+    uint4 kAlo[NB], kAhi[NB], vAlo[NB], vAhi[NB], kBlo[NB], kBhi[NB], vBlo[NB], vBhi[NB];
+    fetch_idx();
+#pragma unroll
+    for (int u = 0; u < NB; ++u) { ld16<DT>(kb, ko[u], kAlo[u], kAhi[u]); ld16<DT>(vb, vo[u], vAlo[u], vAhi[u]); }
+    qAlo = qIlo; qAhi = qIhi;
+    advance(ri, qi);
+    if (ntask > 1) fetch_idx();
+    for (int tau = 0; tau < ntask; tau += 2) {
+        if (tau + 1 < ntask) {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) { ld16<DT>(kb, ko[u], kBlo[u], kBhi[u]); ld16<DT>(vb, vo[u], vBlo[u], vBhi[u]); }
+            qBlo = qIlo; qBhi = qIhi;
+            advance(ri, qi);
+            if (tau + 2 < ntask) fetch_idx();
+        }
+        compute(kAlo, kAhi, vAlo, vAhi, qAlo, qAhi);
+        if (tau + 1 < ntask) {
+            if (tau + 2 < ntask) {
+#pragma unroll
+                for (int u = 0; u < NB; ++u) { ld16<DT>(kb, ko[u], kAlo[u], kAhi[u]); ld16<DT>(vb, vo[u], vAlo[u], vAhi[u]); }
+                qAlo = qIlo; qAhi = qIhi;
+                advance(ri, qi);
+                if (tau + 3 < ntask) fetch_idx();
+            }
+            compute(kBlo, kBhi, vBlo, vBhi, qBlo, qBhi);
+        }
+    }
+}
+
+template <typename DT, int D>
+hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
+{
+#ifndef WF_READOUT_FAST_NB
+#define WF_READOUT_FAST_NB 4
+#endif
+    const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
+    sparse_readout_fast<DT, D, WF_READOUT_FAST_NB><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
+    return hipGetLastError();
+}
+
+template <typename DT>
+hipError_t launch_fast_t(const ReadoutParams& p, hipStream_t s)
+{
+    if (p.D == 32) return launch_fast_d<DT, 32>(p, s);
+    if (p.D == 64) return launch_fast_d<DT, 64>(p, s);
+    return launch_fast_d<DT, 128>(p, s);
 }
 
 template <typename DT, bool VEC, int D>
 hipError_t launch_d(const ReadoutParams& p, hipStream_t s)
 {
     const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
-    constexpr int NB = (sizeof(DT) == 4) ? 4 : 8;
+#ifndef WF_READOUT_NB
+#define WF_READOUT_NB 4
+#endif
+    constexpr int NB = WF_READOUT_NB;
     sparse_readout_kernel<DT, VEC, D, NB><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
     return hipGetLastError();
 }
@@ -214,8 +564,13 @@ hipError_t launch_t(bool vec, const ReadoutParams& p, hipStream_t s)
 
 }  // namespace
 
-hipError_t launch_sparse_readout(int dtype, bool vec, const ReadoutParams& p, hipStream_t s)
+hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutParams& p, hipStream_t s)
 {
+    if (fast) {
+        if (dtype == 2) return launch_fast_t<bf16_t>(p, s);
+        if (dtype == 1) return launch_fast_t<_Float16>(p, s);
+        return launch_fast_t<float>(p, s);
+    }
     if (dtype == 2) return launch_t<bf16_t>(vec, p, s);
     if (dtype == 1) return launch_t<_Float16>(vec, p, s);
     return launch_t<float>(vec, p, s);

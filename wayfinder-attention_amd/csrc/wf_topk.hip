@@ -33,8 +33,16 @@
 namespace wf {
 namespace {
 
+#ifndef WF_TOPK_WAVES
+#define WF_TOPK_WAVES 4
+#endif
+#ifndef WF_TOPK_CHECK_EVERY
+#define WF_TOPK_CHECK_EVERY 1
+#endif
+
 constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
-constexpr int kWaves = 4;                              // waves per workgroup (split the keys)
+constexpr int kWaves = WF_TOPK_WAVES;                  // waves per workgroup (split the keys)
+constexpr int kCheckEvery = WF_TOPK_CHECK_EVERY;       // key steps between pool-fill checks
 constexpr int kBins = 128;                             // pruning histogram bins per row
 constexpr int kPrefetch = 4;                           // key steps each wave loads ahead
 constexpr float kEpsRel = 1.0f / 4096.0f;              // 2^-12: > 20x the MFMA/FMA error bound
@@ -463,13 +471,14 @@ template <typename DT, bool VEC, int RC, int KP2>
 __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 {
     constexpr int RP = RC * 32;
-    constexpr int POOL = KP2 + 256;
-    constexpr int LIMIT = POOL - 16 * kWaves;   // a step appends <= 16 per row per wave
+    constexpr int MARGIN = 16 * kWaves * kCheckEvery;   // a step appends <= 16 per row per wave
+    constexpr int POOL = KP2 + 192 + MARGIN;
+    constexpr int LIMIT = POOL - MARGIN;
     constexpr int HEADROOM = 64;                 // a prune must leave this much room
     __shared__ TopkSmem<RP, POOL> sm;
 
     const int lane = lane_id();
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     // screening layout: MFMA column n = query row, lane group g = dims 8g..8g+7 / keys 4g..4g+3
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -566,10 +575,11 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
                     }
                 }
             }
+            if ((it + 1) % kCheckEvery != 0 && it + 1 != iters) continue;
             __syncthreads();
             const bool over = lane < kRows && sm.cnt[lane] > LIMIT;
             if (__ballot(over)) {   // same decision in every wave: all read after the barrier
-                const int c = sm.cnt[rr];
+                const int c = rr < kRows ? sm.cnt[rr] : 0;
                 if (c > K) {
                     int c2 = c;
                     const bool ok = prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr],
@@ -587,7 +597,7 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 
     // ---- finish: prune, rescore exactly, select, sort, write
     __syncthreads();
-    if (r0 + rr < T) {
+    if (rr < kRows && r0 + rr < T) {
         int c = sm.cnt[rr];
         if (c > K) {
             int c2 = c;
