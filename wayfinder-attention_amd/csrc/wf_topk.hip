@@ -28,6 +28,8 @@
 // K-th score >= theta' - eps, so s_K >= theta' - eps and every key that can still enter E
 // (exact score >= s_K, ties included since waves see keys out of index order) has MFMA
 // score >= theta' - 2 eps = the threshold. The final choice uses exact scores only.
+#include <type_traits>
+
 #include "wf_internal.h"
 
 namespace wf {
@@ -37,7 +39,7 @@ namespace {
 #define WF_TOPK_WAVES 4
 #endif
 #ifndef WF_TOPK_CHECK_EVERY
-#define WF_TOPK_CHECK_EVERY 1
+#define WF_TOPK_CHECK_EVERY 2
 #endif
 
 constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
@@ -472,7 +474,7 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 {
     constexpr int RP = RC * 32;
     constexpr int MARGIN = 16 * kWaves * kCheckEvery;   // a step appends <= 16 per row per wave
-    constexpr int POOL = KP2 + 192 + MARGIN;
+    constexpr int POOL = KP2 + (KP2 >= 256 ? 128 : 192) + MARGIN;   // 2 workgroups per CU
     constexpr int LIMIT = POOL - MARGIN;
     constexpr int HEADROOM = 64;                 // a prune must leave this much room
     __shared__ TopkSmem<RP, POOL> sm;
@@ -529,51 +531,78 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
     __syncthreads();
 
     // ---- screen
-    float th = -__builtin_inff();
-    const int64_t nsteps = last / 16 + 1;
-    const int64_t iters = (nsteps + kWaves - 1) / kWaves;
+    // rows past T never take candidates; their threshold is +inf
+    float th = row_ok ? -__builtin_inff() : __builtin_inff();
+    const int Ti = int(T);
+    const int rowi = int(row);
+    const int r0i = int(r0);
+    const int nsteps = int(last / 16) + 1;
+    const int iters = (nsteps + kWaves - 1) / kWaves;
+    // key rows are read at 32-bit byte offsets from the batch base (VEC layouts only)
+    const char* kbytes = reinterpret_cast<const char*>(kb);
+    const uint32_t krow = uint32_t(p.kst) * uint32_t(sizeof(DT));
+    auto load_step = [&](int st, uint4 (&lo)[RC], uint4 (&hi)[RC]) {
+        const int j = min(st * 16 + n, Ti - 1);
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+            const int d0 = 32 * c + 8 * g;
+            if constexpr (VEC) {
+                lo[c] = make_uint4(0, 0, 0, 0);
+                hi[c] = lo[c];
+                if (d0 < R) {
+                    const uint32_t off = uint32_t(j) * krow + uint32_t(d0) * uint32_t(sizeof(DT));
+                    lo[c] = *reinterpret_cast<const uint4*>(kbytes + off);
+                    if constexpr (sizeof(DT) == 4) hi[c] = *reinterpret_cast<const uint4*>(kbytes + off + 16u);
+                }
+            } else {
+                load8<DT, false>(kb + int64_t(j) * p.kst, p.ksr, d0, R, lo[c], hi[c]);
+            }
+        }
+    };
+    // score one 16-key step and append the candidates that reach the threshold (one LDS
+    // atomic per lane for its up to 4 candidates)
+    auto screen = [&](auto diag_tag, int st, const uint4 (&alo)[RC], const uint4 (&ahi)[RC]) {
+        constexpr bool DIAG = decltype(diag_tag)::value;
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < RC; ++c) acc = mfma_chunk<DT>(alo[c], ahi[c], qlo[c], qhi[c], acc);
+        const int jb = st * 16 + 4 * g;
+        bool pp[4];
+        int cntp = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pp[i] = acc[i] >= th && (!DIAG || jb + i <= rowi);
+            cntp += pp[i] ? 1 : 0;
+        }
+        if (cntp) {
+            int pos = atomicAdd(&sm.cnt[n], cntp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (pp[i]) sm.pool[n][pos++] = Entry{acc[i], uint32_t(jb + i)};
+        }
+    };
     uint4 plo[kPrefetch][RC], phi[kPrefetch][RC];
 #pragma unroll
     for (int v = 0; v < kPrefetch; ++v) {
-        const int64_t st = w + int64_t(kWaves) * v;
-        const int64_t j = min(st * 16 + n, T - 1);
+        const int st = w + kWaves * v;
 #pragma unroll
-        for (int c = 0; c < RC; ++c) {
-            plo[v][c] = make_uint4(0, 0, 0, 0);
-            phi[v][c] = plo[v][c];
-            if (st < nsteps) load8<DT, VEC>(kb + j * p.kst, p.ksr, 32 * c + 8 * g, R, plo[v][c], phi[v][c]);
-        }
+        for (int c = 0; c < RC; ++c) { plo[v][c] = make_uint4(0, 0, 0, 0); phi[v][c] = plo[v][c]; }
+        if (st < nsteps) load_step(st, plo[v], phi[v]);
     }
-    for (int64_t it0 = 0; it0 < iters; it0 += kPrefetch) {
+    for (int it0 = 0; it0 < iters; it0 += kPrefetch) {
 #pragma unroll
         for (int v = 0; v < kPrefetch; ++v) {
-            const int64_t it = it0 + v;
+            const int it = it0 + v;
             if (it >= iters) break;
-            const int64_t st = w + int64_t(kWaves) * it;
+            const int st = w + kWaves * it;
             if (st < nsteps) {
                 uint4 alo[RC], ahi[RC];
 #pragma unroll
                 for (int c = 0; c < RC; ++c) { alo[c] = plo[v][c]; ahi[c] = phi[v][c]; }
-                const int64_t stn = st + int64_t(kWaves) * kPrefetch;
-                if (stn < nsteps) {
-                    const int64_t j = min(stn * 16 + n, T - 1);
-#pragma unroll
-                    for (int c = 0; c < RC; ++c)
-                        load8<DT, VEC>(kb + j * p.kst, p.ksr, 32 * c + 8 * g, R, plo[v][c], phi[v][c]);
-                }
-                f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int c = 0; c < RC; ++c) acc = mfma_chunk<DT>(alo[c], ahi[c], qlo[c], qhi[c], acc);
-                const int64_t j0 = st * 16;
-                const bool diag = (j0 == r0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int64_t j = j0 + 4 * g + i;
-                    if (row_ok && acc[i] >= th && (!diag || j <= row)) {
-                        const int pos = atomicAdd(&sm.cnt[n], 1);
-                        sm.pool[n][pos] = Entry{acc[i], uint32_t(j)};
-                    }
-                }
+                const int stn = st + kWaves * kPrefetch;
+                if (stn < nsteps) load_step(stn, plo[v], phi[v]);
+                if (st * 16 == r0i) screen(std::true_type{}, st, alo, ahi);
+                else screen(std::false_type{}, st, alo, ahi);
             }
             if ((it + 1) % kCheckEvery != 0 && it + 1 != iters) continue;
             __syncthreads();
@@ -590,7 +619,7 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
                                                      p.ksr, R, K, u);
                 }
                 __syncthreads();
-                th = sm.thr[n];
+                th = row_ok ? sm.thr[n] : __builtin_inff();
             }
         }
     }
