@@ -38,13 +38,9 @@ namespace {
 #ifndef WF_TOPK_WAVES
 #define WF_TOPK_WAVES 4
 #endif
-#ifndef WF_TOPK_CHECK_EVERY
-#define WF_TOPK_CHECK_EVERY 2
-#endif
 
 constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
 constexpr int kWaves = WF_TOPK_WAVES;                  // waves per workgroup (split the keys)
-constexpr int kCheckEvery = WF_TOPK_CHECK_EVERY;       // key steps between pool-fill checks
 constexpr int kBins = 128;                             // pruning histogram bins per row
 constexpr int kPrefetch = 4;                           // key steps each wave loads ahead
 constexpr float kEpsRel = 1.0f / 4096.0f;              // 2^-12: > 20x the MFMA/FMA error bound
@@ -129,18 +125,27 @@ __device__ __forceinline__ f32x4_t mfma_chunk(const uint4& alo, const uint4& ahi
 }
 
 // Exact score: acc = fmaf(q[d], k[d], acc) for d = 0..R-1 from acc = 0 (q in LDS as fp32).
-template <typename DT, bool VEC>
+// RP (a multiple of 32) bounds R; every key chunk is loaded before the chain starts.
+template <typename DT, bool VEC, int RP>
 __device__ __forceinline__ float exact_score(const float* q, const DT* krow, int64_t sr, int R)
 {
     float acc = 0.0f;
     if constexpr (VEC) {
-        for (int d0 = 0; d0 < R; d0 += 8) {
-            uint4 lo, hi;
-            load8<DT, true>(krow, 1, d0, R, lo, hi);
+        constexpr int NC = RP / 8;
+        uint4 lo[NC], hi[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            lo[c] = make_uint4(0, 0, 0, 0);
+            hi[c] = lo[c];
+            if (8 * c < R) load8<DT, true>(krow, 1, 8 * c, R, lo[c], hi[c]);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (8 * c >= R) break;
             float kf[8];
-            to_f32x8<DT>(lo, hi, kf);
-            const float4 qa = *reinterpret_cast<const float4*>(q + d0);
-            const float4 qb = *reinterpret_cast<const float4*>(q + d0 + 4);
+            to_f32x8<DT>(lo[c], hi[c], kf);
+            const float4 qa = *reinterpret_cast<const float4*>(q + 8 * c);
+            const float4 qb = *reinterpret_cast<const float4*>(q + 8 * c + 4);
             acc = fmaf(qa.x, kf[0], acc); acc = fmaf(qa.y, kf[1], acc);
             acc = fmaf(qa.z, kf[2], acc); acc = fmaf(qa.w, kf[3], acc);
             acc = fmaf(qb.x, kf[4], acc); acc = fmaf(qb.y, kf[5], acc);
@@ -159,51 +164,93 @@ __device__ __forceinline__ uint64_t make_key(float s, uint32_t j)
 
 // ------------------------------------------------------------------ 16-lane row groups
 // In the row-parallel phases query row r of the block is owned by lanes 16*(r%4)..+15 of
-// wave r/4, i.e. by one 16-lane DPP row, so all cross-lane traffic stays inside a wave.
+// wave r/4, i.e. by one 16-lane DPP row, so every cross-lane step is a DPP move (no LDS
+// round trip): row_ror rotations for all-reduces, row_shl shifts for suffix scans.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t x)
+{
+    return uint32_t(__builtin_amdgcn_mov_dpp(int(x), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>   // shifted-in lanes read 0
+__device__ __forceinline__ uint32_t dpp32z(uint32_t x)
+{
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), CTRL, 0xf, 0xf, true));
+}
+constexpr int kRor8 = 0x128, kRor4 = 0x124, kRor2 = 0x122, kRor1 = 0x121;
+
 __device__ __forceinline__ float row_max16(float x)
 {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 16));
+    x = fmaxf(x, __uint_as_float(dpp32<kRor8>(__float_as_uint(x))));
+    x = fmaxf(x, __uint_as_float(dpp32<kRor4>(__float_as_uint(x))));
+    x = fmaxf(x, __uint_as_float(dpp32<kRor2>(__float_as_uint(x))));
+    x = fmaxf(x, __uint_as_float(dpp32<kRor1>(__float_as_uint(x))));
     return x;
 }
 __device__ __forceinline__ float row_min16(float x)
 {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) x = fminf(x, __shfl_xor(x, o, 16));
+    x = fminf(x, __uint_as_float(dpp32<kRor8>(__float_as_uint(x))));
+    x = fminf(x, __uint_as_float(dpp32<kRor4>(__float_as_uint(x))));
+    x = fminf(x, __uint_as_float(dpp32<kRor2>(__float_as_uint(x))));
+    x = fminf(x, __uint_as_float(dpp32<kRor1>(__float_as_uint(x))));
     return x;
 }
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m, int width)
+__device__ __forceinline__ int row_max16_i32(int x)
 {
-    const uint32_t lo = __shfl_xor(uint32_t(x), m, width);
-    const uint32_t hi = __shfl_xor(uint32_t(x >> 32), m, width);
-    return (uint64_t(hi) << 32) | lo;
+    x = max(x, int(dpp32<kRor8>(uint32_t(x))));
+    x = max(x, int(dpp32<kRor4>(uint32_t(x))));
+    x = max(x, int(dpp32<kRor2>(uint32_t(x))));
+    x = max(x, int(dpp32<kRor1>(uint32_t(x))));
+    return x;
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t x)
+{
+    return (uint64_t(dpp32<CTRL>(uint32_t(x >> 32))) << 32) | dpp32<CTRL>(uint32_t(x));
 }
 __device__ __forceinline__ uint64_t row_max16_u64(uint64_t x)
 {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) { const uint64_t y = shfl_xor_u64(x, o, 16); x = y > x ? y : x; }
+    uint64_t y;
+    y = dpp64<kRor8>(x); x = y > x ? y : x;
+    y = dpp64<kRor4>(x); x = y > x ? y : x;
+    y = dpp64<kRor2>(x); x = y > x ? y : x;
+    y = dpp64<kRor1>(x); x = y > x ? y : x;
     return x;
 }
 __device__ __forceinline__ uint64_t row_min16_u64(uint64_t x)
 {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) { const uint64_t y = shfl_xor_u64(x, o, 16); x = y < x ? y : x; }
+    uint64_t y;
+    y = dpp64<kRor8>(x); x = y < x ? y : x;
+    y = dpp64<kRor4>(x); x = y < x ? y : x;
+    y = dpp64<kRor2>(x); x = y < x ? y : x;
+    y = dpp64<kRor1>(x); x = y < x ? y : x;
     return x;
 }
-// sum of x over the lanes of the row with a higher sub-lane index
-__device__ __forceinline__ int row_suffix_excl16(int x, int u)
+// sum of x over the lanes of the row with a higher sub-lane index (row_shl:n brings lane
+// i+n to lane i, zero past the end of the row)
+__device__ __forceinline__ int row_suffix_excl16(int x)
 {
-    int s = x;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        const int y = __shfl_down(s, o, 16);
-        if (u + o < 16) s += y;
-    }
-    return s - x;
+    uint32_t s = uint32_t(x);
+    s += dpp32z<0x101>(s);
+    s += dpp32z<0x102>(s);
+    s += dpp32z<0x104>(s);
+    s += dpp32z<0x108>(s);
+    return int(s) - x;
 }
 __device__ __forceinline__ uint32_t row_bits16(uint64_t ballot)
 {
     return uint32_t(ballot >> (lane_id() & 48)) & 0xffffu;
+}
+// value of lane u ^ LX within the 16-lane row (LX in {1, 2, 4, 8})
+template <int LX>
+__device__ __forceinline__ uint64_t xor16_u64(uint64_t x, int u)
+{
+    if constexpr (LX == 1) return dpp64<0xB1>(x);       // quad_perm [1,0,3,2]
+    else if constexpr (LX == 2) return dpp64<0x4E>(x);  // quad_perm [2,3,0,1]
+    else if constexpr (LX == 8) return dpp64<kRor8>(x);
+    else {                                              // row_ror:4 / :12, by lane
+        const uint64_t a = dpp64<kRor4>(x), b = dpp64<0x12C>(x);
+        return (u & 4) ? a : b;
+    }
 }
 
 struct Entry {
@@ -222,7 +269,8 @@ struct TopkSmem {
 };
 
 // Largest bin b (of the row's kBins-bin histogram) whose suffix count C(b) reaches `need`;
-// also C(b+1) (entries strictly above) and the count of bin b.
+// also C(b+1) (entries strictly above) and the count of bin b. Exactly one lane of the row
+// holds the crossing; its values reach the other lanes through row maxima.
 __device__ __forceinline__ void find_boundary(const uint32_t* hist, int u, int need, int& b,
                                               int& gt, int& eq)
 {
@@ -233,7 +281,7 @@ __device__ __forceinline__ void find_boundary(const uint32_t* hist, int u, int n
     int tot = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) tot += h[k];
-    const int above = row_suffix_excl16(tot, u);
+    const int above = row_suffix_excl16(tot);
     const bool has = above < need && above + tot >= need;
     int cum = above, bb = -1, g = 0, e = 0;
 #pragma unroll
@@ -241,11 +289,9 @@ __device__ __forceinline__ void find_boundary(const uint32_t* hist, int u, int n
         if (bb < 0 && cum + h[k] >= need) { bb = 8 * u + k; g = cum; e = h[k]; }
         cum += h[k];
     }
-    const uint32_t bits = row_bits16(__ballot(has));
-    const int src = __ffs(bits) - 1;
-    b = __shfl(bb, src, 16);
-    gt = __shfl(g, src, 16);
-    eq = __shfl(e, src, 16);
+    b = row_max16_i32(has ? bb : -1);
+    gt = row_max16_i32(has ? g : -1);
+    eq = row_max16_i32(has ? e : -1);
 }
 
 // Entry <-> 64-bit selection key: (order-preserving score bits, complemented index), so a
@@ -318,9 +364,14 @@ __device__ int exact_row(Entry (&pool)[POOL], uint32_t* hist, int c, int& cnt, f
                          int K, int u)
 {
     constexpr int EPR = POOL / 16;
-    for (int e = u; e < c; e += 16) {
-        const uint32_t j = pool[e].j;
-        pool[e].s = exact_score<DT, VEC>(q, kb + int64_t(j) * kst, ksr, R);
+    for (int e = u; e < c; e += 32) {   // two independent chains per iteration
+        const bool two = e + 16 < c;
+        const uint32_t j0 = pool[e].j;
+        const uint32_t j1 = two ? pool[e + 16].j : j0;
+        const float s0 = exact_score<DT, VEC, RP>(q, kb + int64_t(j0) * kst, ksr, R);
+        const float s1 = exact_score<DT, VEC, RP>(q, kb + int64_t(j1) * kst, ksr, R);
+        pool[e].s = s0;
+        if (two) pool[e + 16].s = s1;
     }
     uint64_t key[EPR];
 #pragma unroll
@@ -408,11 +459,14 @@ __device__ void emit_row(const Entry (&pool)[POOL], int kept, int64_t row, int64
                     key[m2] = desc ? lo : hi;
                 }
             } else {
-                const int lx = jj / EPL;
+                const int lx = jj / EPL;   // folds to a constant once the loops unroll
 #pragma unroll
                 for (int m = 0; m < EPL; ++m) {
                     const int i = u * EPL + m;
-                    const uint64_t other = shfl_xor_u64(key[m], lx, 16);
+                    const uint64_t other = lx == 1 ? xor16_u64<1>(key[m], u)
+                                         : lx == 2 ? xor16_u64<2>(key[m], u)
+                                         : lx == 4 ? xor16_u64<4>(key[m], u)
+                                                   : xor16_u64<8>(key[m], u);
                     const bool low = (i & jj) == 0;
                     const bool desc = (i & kk) == 0;
                     const uint64_t hi = key[m] > other ? key[m] : other;
@@ -473,8 +527,8 @@ template <typename DT, bool VEC, int RC, int KP2>
 __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 {
     constexpr int RP = RC * 32;
-    constexpr int MARGIN = 16 * kWaves * kCheckEvery;   // a step appends <= 16 per row per wave
-    constexpr int POOL = KP2 + (KP2 >= 256 ? 128 : 192) + MARGIN;   // 2 workgroups per CU
+    constexpr int MARGIN = 16 * kWaves;   // one step appends <= 16 per row per wave
+    constexpr int POOL = KP2 + (KP2 >= 256 ? 192 : 256) + MARGIN;   // 2 workgroups per CU
     constexpr int LIMIT = POOL - MARGIN;
     constexpr int HEADROOM = 64;                 // a prune must leave this much room
     __shared__ TopkSmem<RP, POOL> sm;
@@ -530,6 +584,10 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
     }
     __syncthreads();
 
+#ifdef WF_TOPK_TIMING
+    uint64_t tm0 = wall_clock64();
+    uint64_t tcomp = 0, ncomp = 0;
+#endif
     // ---- screen
     // rows past T never take candidates; their threshold is +inf
     float th = row_ok ? -__builtin_inff() : __builtin_inff();
@@ -581,6 +639,7 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
                 if (pp[i]) sm.pool[n][pos++] = Entry{acc[i], uint32_t(jb + i)};
         }
     };
+    int budget = max(1, POOL / (16 * kWaves));   // steps until the next pool check
     uint4 plo[kPrefetch][RC], phi[kPrefetch][RC];
 #pragma unroll
     for (int v = 0; v < kPrefetch; ++v) {
@@ -604,10 +663,14 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
                 if (st * 16 == r0i) screen(std::true_type{}, st, alo, ahi);
                 else screen(std::false_type{}, st, alo, ahi);
             }
-            if ((it + 1) % kCheckEvery != 0 && it + 1 != iters) continue;
+            if (--budget > 0 && it + 1 != iters) continue;
             __syncthreads();
-            const bool over = lane < kRows && sm.cnt[lane] > LIMIT;
+            const int cl = lane < kRows ? sm.cnt[lane] : 0;
+            const bool over = cl > LIMIT;
             if (__ballot(over)) {   // same decision in every wave: all read after the barrier
+#ifdef WF_TOPK_TIMING
+                const uint64_t tc0 = wall_clock64();
+#endif
                 const int c = rr < kRows ? sm.cnt[rr] : 0;
                 if (c > K) {
                     int c2 = c;
@@ -620,12 +683,26 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
                 }
                 __syncthreads();
                 th = row_ok ? sm.thr[n] : __builtin_inff();
+#ifdef WF_TOPK_TIMING
+                tcomp += wall_clock64() - tc0;
+                ++ncomp;
+#endif
+            }
+            // steps every wave may take before the pools can overflow (each step appends
+            // at most 16 candidates per row per wave); read after the barrier by all waves
+            {
+                const int cmax = __builtin_amdgcn_readfirstlane(
+                    row_max16_i32(lane < kRows ? sm.cnt[lane] : 0));
+                budget = max(1, (POOL - cmax) / (16 * kWaves));
             }
         }
     }
 
     // ---- finish: prune, rescore exactly, select, sort, write
     __syncthreads();
+#ifdef WF_TOPK_TIMING
+    uint64_t tm1 = wall_clock64();
+#endif
     if (rr < kRows && r0 + rr < T) {
         int c = sm.cnt[rr];
         if (c > K) {
@@ -636,9 +713,21 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
         const int kept = exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c, sm.cnt[rr],
                                                       sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
                                                       p.ksr, R, K, u);
+#ifdef WF_TOPK_TIMING
+        emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, p.out_idx + b * T * p.k_eff,
+                            nullptr, u);
+#else
         emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, p.out_idx + b * T * p.k_eff,
                             p.out_scores ? p.out_scores + b * T * p.k_eff : nullptr, u);
+#endif
     }
+#ifdef WF_TOPK_TIMING
+    __syncthreads();
+    if (threadIdx.x == 0 && p.out_scores) {
+        uint64_t* tm = reinterpret_cast<uint64_t*>(p.out_scores) + 4 * blockIdx.x;
+        tm[0] = tm0; tm[1] = tm1; tm[2] = wall_clock64(); tm[3] = uint64_t(rb) | (ncomp << 16) | (tcomp << 32);
+    }
+#endif
 }
 
 template <typename DT, bool VEC, int RC>
