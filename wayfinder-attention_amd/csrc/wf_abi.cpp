@@ -125,8 +125,10 @@ int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T
     p.chunk_absmax = static_cast<float*>(ws);
     p.n_chunks = cdiv(T, wf::kAbsmaxChunk);
     p.n_row_blocks = cdiv(T, 16);
-    // vector loads; key rows are addressed with 32-bit byte offsets from the batch base
-    const bool vec = vec_ok(query, dtype, qs, 3, R) && vec_ok(key, dtype, ks, 3, R) &&
+    // vector loads; key rows are addressed with 32-bit byte offsets from the batch base and
+    // every 32-dim chunk the kernel reads lies inside the row (R = 32, 64 or 128)
+    const bool vec = (R == 32 || R == 64 || R == 128) &&
+                     vec_ok(query, dtype, qs, 3, R) && vec_ok(key, dtype, ks, 3, R) &&
                      ks[1] >= 0 && (T - 1) * ks[1] * int64_t(elem_size(dtype)) + R * int64_t(elem_size(dtype)) < (int64_t(1) << 32);
     hipError_t e = wf::launch_key_absmax(dtype, vec, p, stream);
     if (e != hipSuccess) return hip_fail("causal_topk: key magnitude kernel launch", e);

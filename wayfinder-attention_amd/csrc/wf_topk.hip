@@ -42,7 +42,8 @@ namespace {
 constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
 constexpr int kWaves = WF_TOPK_WAVES;                  // waves per workgroup (split the keys)
 constexpr int kBins = 128;                             // pruning histogram bins per row
-constexpr int kPrefetch = 4;                           // key steps each wave loads ahead
+constexpr int kPD = 4;                                 // key steps each wave keeps in flight
+constexpr int kUnitMax = 2 * 16 * kWaves;              // appends per row in one 2-step unit, at most
 constexpr float kEpsRel = 1.0f / 4096.0f;              // 2^-12: > 20x the MFMA/FMA error bound
 constexpr float kTiny = 7.888609052210118e-31f;        // 2^-100: covers denormal flushing
 
@@ -261,7 +262,7 @@ struct Entry {
 template <int RP, int POOL>
 struct TopkSmem {
     float q[kRows][RP];            // fp32 query rows (exact rescoring)
-    Entry pool[kRows][POOL];       // candidate pool per row
+    Entry pool[kRows][POOL + 1];   // candidate pool per row (+ a dummy slot for non-candidates)
     uint32_t hist[kRows][kBins];   // per-row histogram (pruning and radix select)
     int cnt[kRows];                // pool fill
     float thr[kRows];              // screening threshold (-inf until K candidates are known)
@@ -306,7 +307,7 @@ __device__ __forceinline__ Entry key_entry(uint64_t k)
 // pool is cut to the entries >= theta' - 2 eps, c_out is the new count (uniform over the
 // row's lanes) and, from lane u == 0, cnt / thr are stored for the other waves.
 template <int POOL>
-__device__ bool prune_row(Entry (&pool)[POOL], uint32_t* hist, int c, int& c_out, int& cnt,
+__device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& cnt,
                           float& thr, float eps, int K, int u)
 {
     constexpr int EPR = POOL / 16;
@@ -359,7 +360,7 @@ __device__ bool prune_row(Entry (&pool)[POOL], uint32_t* hist, int c, int& c_out
 // (score desc, index asc); the winners end up in pool[0..kept) with exact scores. Returns
 // kept (uniform over the row); lane u == 0 stores cnt and the exact threshold s_K - eps.
 template <typename DT, bool VEC, int RP, int POOL>
-__device__ int exact_row(Entry (&pool)[POOL], uint32_t* hist, int c, int& cnt, float& thr,
+__device__ int exact_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& thr,
                          float eps, const float* q, const DT* kb, int64_t kst, int64_t ksr, int R,
                          int K, int u)
 {
@@ -433,7 +434,7 @@ __device__ int exact_row(Entry (&pool)[POOL], uint32_t* hist, int c, int& cnt, f
 // Sort row r's (exactly scored) winners into canonical order and write them plus pads.
 // `row` is the query position t in its batch; out_idx/out_scores point at the batch.
 template <int KP2, int POOL>
-__device__ void emit_row(const Entry (&pool)[POOL], int kept, int64_t row, int64_t T,
+__device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
                          int64_t k_eff, int32_t* out_idx, float* out_scores, int u)
 {
     constexpr int EPL = KP2 / 16;   // elements per lane; element i = u * EPL + m
@@ -527,10 +528,12 @@ template <typename DT, bool VEC, int RC, int KP2>
 __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 {
     constexpr int RP = RC * 32;
-    constexpr int MARGIN = 16 * kWaves;   // one step appends <= 16 per row per wave
-    constexpr int POOL = KP2 + (KP2 >= 256 ? 192 : 256) + MARGIN;   // 2 workgroups per CU
-    constexpr int LIMIT = POOL - MARGIN;
+    // pool entries per row: two workgroups (<= 80 KiB of LDS each) per CU
+    constexpr int POOL = RP <= 64 ? 512 : 496;
+    constexpr int LIMIT = POOL - kUnitMax;       // a pool above this is pruned at the next check
     constexpr int HEADROOM = 64;                 // a prune must leave this much room
+    static_assert(LIMIT - HEADROOM > KP2 + 32, "pool too small for K");
+    static_assert(sizeof(TopkSmem<RP, POOL>) <= 80 * 1024, "two workgroups per CU");
     __shared__ TopkSmem<RP, POOL> sm;
 
     const int lane = lane_id();
@@ -589,115 +592,135 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
     uint64_t tcomp = 0, ncomp = 0;
 #endif
     // ---- screen
+    // Steps 0 .. nfull-1 hold keys below the block's first row r0, so they need neither a
+    // causal mask nor clamping; step nfull (the diagonal, keys r0 .. r0+15) is taken once,
+    // after the loop, by wave nfull % kWaves. The loop keeps kPD key loads in flight per wave
+    // in distinct registers (the unrolled v) and never waits for more than the oldest.
     // rows past T never take candidates; their threshold is +inf
     float th = row_ok ? -__builtin_inff() : __builtin_inff();
     const int Ti = int(T);
     const int rowi = int(row);
     const int r0i = int(r0);
     const int nsteps = int(last / 16) + 1;
-    const int iters = (nsteps + kWaves - 1) / kWaves;
+    const int nfull = nsteps - 1;
+    const int iters = (nfull + kWaves - 1) / kWaves;   // equal in every wave: barriers match
     // key rows are read at 32-bit byte offsets from the batch base (VEC layouts only)
     const char* kbytes = reinterpret_cast<const char*>(kb);
     const uint32_t krow = uint32_t(p.kst) * uint32_t(sizeof(DT));
-    auto load_step = [&](int st, uint4 (&lo)[RC], uint4 (&hi)[RC]) {
-        const int j = min(st * 16 + n, Ti - 1);
+    const uint32_t lane_off = uint32_t(n) * krow + uint32_t(8 * g) * uint32_t(sizeof(DT));
+    // keys j0 + n of one step; VEC requires R % 32 == 0, so every lane's dims are inside R
+    auto load_step = [&](int j0, uint4 (&lo)[RC], uint4 (&hi)[RC]) {
 #pragma unroll
         for (int c = 0; c < RC; ++c) {
-            const int d0 = 32 * c + 8 * g;
             if constexpr (VEC) {
-                lo[c] = make_uint4(0, 0, 0, 0);
-                hi[c] = lo[c];
-                if (d0 < R) {
-                    const uint32_t off = uint32_t(j) * krow + uint32_t(d0) * uint32_t(sizeof(DT));
-                    lo[c] = *reinterpret_cast<const uint4*>(kbytes + off);
-                    if constexpr (sizeof(DT) == 4) hi[c] = *reinterpret_cast<const uint4*>(kbytes + off + 16u);
-                }
+                const uint32_t off = uint32_t(j0) * krow + lane_off + uint32_t(32 * c * sizeof(DT));
+                lo[c] = *reinterpret_cast<const uint4*>(kbytes + off);
+                if constexpr (sizeof(DT) == 4) hi[c] = *reinterpret_cast<const uint4*>(kbytes + off + 16u);
+                else hi[c] = make_uint4(0, 0, 0, 0);
             } else {
-                load8<DT, false>(kb + int64_t(j) * p.kst, p.ksr, d0, R, lo[c], hi[c]);
+                const int j = min(j0 + n, Ti - 1);
+                load8<DT, false>(kb + int64_t(j) * p.kst, p.ksr, 32 * c + 8 * g, R, lo[c], hi[c]);
             }
         }
     };
-    // score one 16-key step and append the candidates that reach the threshold (one LDS
-    // atomic per lane for its up to 4 candidates)
-    auto screen = [&](auto diag_tag, int st, const uint4 (&alo)[RC], const uint4 (&ahi)[RC]) {
-        constexpr bool DIAG = decltype(diag_tag)::value;
+    // append the lane's candidates (keys jb .. jb+3 of row n) that reach the threshold; one
+    // LDS atomic reserves their slots, the others are written to the row's dummy slot POOL
+    auto append = [&](const f32x4_t& acc, const bool (&pp)[4], int jb) {
+        const int cntp = int(pp[0]) + int(pp[1]) + int(pp[2]) + int(pp[3]);
+        int pos = atomicAdd(&sm.cnt[n], cntp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sm.pool[n][pp[i] ? pos : POOL] = Entry{acc[i], uint32_t(jb + i)};
+            pos += int(pp[i]);
+        }
+    };
+    auto consider = [&](const f32x4_t& acc, int jb) {
+        const bool pp[4] = {acc[0] >= th, acc[1] >= th, acc[2] >= th, acc[3] >= th};
+        if (pp[0] || pp[1] || pp[2] || pp[3]) append(acc, pp, jb);
+    };
+    auto score = [&](const uint4 (&alo)[RC], const uint4 (&ahi)[RC]) {
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < RC; ++c) acc = mfma_chunk<DT>(alo[c], ahi[c], qlo[c], qhi[c], acc);
-        const int jb = st * 16 + 4 * g;
-        bool pp[4];
-        int cntp = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pp[i] = acc[i] >= th && (!DIAG || jb + i <= rowi);
-            cntp += pp[i] ? 1 : 0;
-        }
-        if (cntp) {
-            int pos = atomicAdd(&sm.cnt[n], cntp);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (pp[i]) sm.pool[n][pos++] = Entry{acc[i], uint32_t(jb + i)};
-        }
+        return acc;
     };
-    int budget = max(1, POOL / (16 * kWaves));   // steps until the next pool check
-    uint4 plo[kPrefetch][RC], phi[kPrefetch][RC];
-#pragma unroll
-    for (int v = 0; v < kPrefetch; ++v) {
-        const int st = w + kWaves * v;
-#pragma unroll
-        for (int c = 0; c < RC; ++c) { plo[v][c] = make_uint4(0, 0, 0, 0); phi[v][c] = plo[v][c]; }
-        if (st < nsteps) load_step(st, plo[v], phi[v]);
-    }
-    for (int it0 = 0; it0 < iters; it0 += kPrefetch) {
-#pragma unroll
-        for (int v = 0; v < kPrefetch; ++v) {
-            const int it = it0 + v;
-            if (it >= iters) break;
-            const int st = w + kWaves * it;
-            if (st < nsteps) {
-                uint4 alo[RC], ahi[RC];
-#pragma unroll
-                for (int c = 0; c < RC; ++c) { alo[c] = plo[v][c]; ahi[c] = phi[v][c]; }
-                const int stn = st + kWaves * kPrefetch;
-                if (stn < nsteps) load_step(stn, plo[v], phi[v]);
-                if (st * 16 == r0i) screen(std::true_type{}, st, alo, ahi);
-                else screen(std::false_type{}, st, alo, ahi);
+    // budget: 2-step units every wave may still take before a pool could overflow (a unit
+    // appends at most kUnitMax per row); equal in every wave, read after barriers
+    int budget = max(1, (POOL - 0) / kUnitMax);
+    auto check = [&]() {
+        __syncthreads();
+        const int cl = lane < kRows ? sm.cnt[lane] : 0;
+        if (__ballot(cl > LIMIT)) {   // same decision in every wave: all read after the barrier
+#ifdef WF_TOPK_TIMING
+            const uint64_t tc0 = wall_clock64();
+#endif
+            const int c = rr < kRows ? sm.cnt[rr] : 0;
+            if (c > K) {
+                int c2 = c;
+                const bool ok = prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr],
+                                                sm.thr[rr], sm.eps[rr], K, u);
+                if (!ok || c2 > LIMIT - HEADROOM)
+                    exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c2, sm.cnt[rr],
+                                                 sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
+                                                 p.ksr, R, K, u);
             }
-            if (--budget > 0 && it + 1 != iters) continue;
             __syncthreads();
-            const int cl = lane < kRows ? sm.cnt[lane] : 0;
-            const bool over = cl > LIMIT;
-            if (__ballot(over)) {   // same decision in every wave: all read after the barrier
+            th = row_ok ? sm.thr[n] : __builtin_inff();
 #ifdef WF_TOPK_TIMING
-                const uint64_t tc0 = wall_clock64();
+            tcomp += wall_clock64() - tc0;
+            ++ncomp;
 #endif
-                const int c = rr < kRows ? sm.cnt[rr] : 0;
-                if (c > K) {
-                    int c2 = c;
-                    const bool ok = prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr],
-                                                    sm.thr[rr], sm.eps[rr], K, u);
-                    if (!ok || c2 > LIMIT - HEADROOM)
-                        exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c2, sm.cnt[rr],
-                                                     sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
-                                                     p.ksr, R, K, u);
-                }
-                __syncthreads();
-                th = row_ok ? sm.thr[n] : __builtin_inff();
-#ifdef WF_TOPK_TIMING
-                tcomp += wall_clock64() - tc0;
-                ++ncomp;
-#endif
-            }
-            // steps every wave may take before the pools can overflow (each step appends
-            // at most 16 candidates per row per wave); read after the barrier by all waves
-            {
-                const int cmax = __builtin_amdgcn_readfirstlane(
-                    row_max16_i32(lane < kRows ? sm.cnt[lane] : 0));
-                budget = max(1, (POOL - cmax) / (16 * kWaves));
+        }
+        const int cmax = __builtin_amdgcn_readfirstlane(
+            row_max16_i32(lane < kRows ? sm.cnt[lane] : 0));
+        budget = max(1, (POOL - cmax) / kUnitMax);
+    };
+    if (iters > 0) {
+        uint4 blo[kPD][RC], bhi[kPD][RC];
+        // issued in buffer order (the scheduler must not reorder them): the loop then waits
+        // for the two oldest loads only
+#pragma unroll
+        for (int v = 0; v < kPD; ++v) {
+            load_step(16 * min(w + kWaves * v, nfull - 1), blo[v], bhi[v]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int it0 = 0; it0 < iters; it0 += kPD) {
+#pragma unroll
+            for (int h = 0; h < kPD; h += 2) {   // one 2-step unit
+                // both MFMAs read their buffers before the refills overwrite them
+                const f32x4_t acc0 = score(blo[h], bhi[h]);
+                const f32x4_t acc1 = score(blo[h + 1], bhi[h + 1]);
+                const int st0 = w + kWaves * (it0 + h);
+                const int st1 = st0 + kWaves;
+                load_step(16 * min(st0 + kWaves * kPD, nfull - 1), blo[h], bhi[h]);
+                load_step(16 * min(st1 + kWaves * kPD, nfull - 1), blo[h + 1], bhi[h + 1]);
+                if (st0 < nfull) consider(acc0, st0 * 16 + 4 * g);
+                if (st1 < nfull) consider(acc1, st1 * 16 + 4 * g);
+                if (--budget == 0) check();
             }
         }
     }
-
+    if (w == nfull % kWaves) {   // the diagonal step: keys r0 .. r0+15, causal mask
+        uint4 alo[RC], ahi[RC];
+        if constexpr (VEC) {
+            // the block's last rows may pass T: clamp those lanes' key to T-1 (masked below)
+            const int j = min(r0i + n, Ti - 1);
+#pragma unroll
+            for (int c = 0; c < RC; ++c) {
+                const uint32_t off = uint32_t(j) * krow + uint32_t(8 * g + 32 * c) * uint32_t(sizeof(DT));
+                alo[c] = *reinterpret_cast<const uint4*>(kbytes + off);
+                if constexpr (sizeof(DT) == 4) ahi[c] = *reinterpret_cast<const uint4*>(kbytes + off + 16u);
+                else ahi[c] = make_uint4(0, 0, 0, 0);
+            }
+        } else {
+            load_step(r0i, alo, ahi);
+        }
+        const f32x4_t acc = score(alo, ahi);
+        const int jb = r0i + 4 * g;
+        const bool pp[4] = {acc[0] >= th && jb <= rowi, acc[1] >= th && jb + 1 <= rowi,
+                            acc[2] >= th && jb + 2 <= rowi, acc[3] >= th && jb + 3 <= rowi};
+        if (pp[0] || pp[1] || pp[2] || pp[3]) append(acc, pp, jb);
+    }
     // ---- finish: prune, rescore exactly, select, sort, write
     __syncthreads();
 #ifdef WF_TOPK_TIMING
