@@ -262,8 +262,12 @@ struct Entry {
 template <int RP, int POOL>
 struct TopkSmem {
     float q[kRows][RP];            // fp32 query rows (exact rescoring)
-    Entry pool[kRows][POOL + 1];   // candidate pool per row (+ a dummy slot for non-candidates)
-    uint32_t hist[kRows][kBins];   // per-row histogram (pruning and radix select)
+    // candidate pool per row + 20 dummy slots (sinks of masked writes: POOL + g for appends,
+    // POOL + 4 + u for prune lanes); a row stride of 1064 dwords spreads rows over the banks
+    Entry pool[kRows][POOL + 20];
+    // per-row histogram (pruning, radix select) + one dummy bin per lane (kBins + u): a masked
+    // atomic lands on its own bank instead of serialising on a shared address
+    uint32_t hist[kRows][kBins + 16];
     int cnt[kRows];                // pool fill
     float thr[kRows];              // screening threshold (-inf until K candidates are known)
     float eps[kRows];              // |MFMA score - exact score| bound of the row
@@ -312,13 +316,19 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
 {
     constexpr int EPR = POOL / 16;
     c_out = c;
+    // every slot is read unconditionally (slots >= c hold stale data and are masked below), so
+    // the reads issue back to back and the row waits on LDS once
+    uint2 ent[EPR];
+#pragma unroll
+    for (int m = 0; m < EPR; ++m) ent[m] = reinterpret_cast<const uint2*>(pool)[u + 16 * m];
+    // masked slots become NaN: every comparison below is false for them (and for NaN scores)
     float s[EPR];
     float lo = __builtin_inff(), hi = -__builtin_inff();
 #pragma unroll
     for (int m = 0; m < EPR; ++m) {
-        const int e = u + 16 * m;
-        s[m] = e < c ? pool[e].s : __builtin_nanf("");
-        if (e < c) { lo = fminf(lo, s[m]); hi = fmaxf(hi, s[m]); }
+        s[m] = u + 16 * m < c ? __uint_as_float(ent[m].x) : __builtin_nanf("");
+        lo = s[m] < lo ? s[m] : lo;
+        hi = s[m] > hi ? s[m] : hi;
     }
     lo = row_min16(lo);
     hi = row_max16(hi);
@@ -328,57 +338,113 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
     reinterpret_cast<uint4*>(hist)[2 * u] = make_uint4(0, 0, 0, 0);
     reinterpret_cast<uint4*>(hist)[2 * u + 1] = make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int m = 0; m < EPR; ++m) {
-        if (u + 16 * m >= c) continue;
+    for (int m = 0; m < EPR; ++m) {   // masked entries count in the lane's dummy bin
         int bin = int((s[m] - lo) * inv);
         bin = bin < 0 ? 0 : (bin > kBins - 1 ? kBins - 1 : bin);
-        atomicAdd(&hist[bin], 1u);
+        atomicAdd(&hist[s[m] >= lo ? bin : kBins + u], 1u);
     }
     int b, gt, eq;
     find_boundary(hist, u, K, b, gt, eq);
     // one bin of slack absorbs the rounding of the bin computation
     const float theta = b >= 1 ? lo + float(b - 1) * (span / float(kBins)) : lo;
     const float kappa = theta - 2.0f * eps;
-    // in-place stream compaction: iteration m reads entries >= 16 m and writes below them
-    int base = 0;
-    const uint32_t lt = (1u << u) - 1u;
+    // compaction: each lane's survivors go, in order, after those of the higher lanes of the
+    // row (all entries are in registers, so the in-place writes cannot clobber unread ones);
+    // dropped entries are written to the lane's dummy slot
+    int mine = 0;
+#pragma unroll
+    for (int m = 0; m < EPR; ++m) mine += s[m] >= kappa ? 1 : 0;
+    int pos = row_suffix_excl16(mine);
+    const int total = row_max16_i32(pos + mine);
 #pragma unroll
     for (int m = 0; m < EPR; ++m) {
-        const int e = u + 16 * m;
-        const bool sel = e < c && s[m] >= kappa;
-        const uint32_t j = sel ? pool[e].j : 0u;
-        const uint32_t bits = row_bits16(__ballot(sel));
-        if (sel) pool[base + __popc(bits & lt)] = Entry{s[m], j};
-        base += __popc(bits);
+        const bool sel = s[m] >= kappa;
+        reinterpret_cast<uint2*>(pool)[sel ? pos : POOL + 4 + u] = ent[m];
+        pos += sel ? 1 : 0;
     }
-    c_out = base;
-    if (u == 0) { cnt = base; thr = kappa; }
+    c_out = total;
+    if (u == 0) { cnt = total; thr = kappa; }
     return true;
 }
 
-// Exact rescoring of a row's c pool entries and exact selection of its min(K, c) best by
-// (score desc, index asc); the winners end up in pool[0..kept) with exact scores. Returns
-// kept (uniform over the row); lane u == 0 stores cnt and the exact threshold s_K - eps.
-template <typename DT, bool VEC, int RP, int POOL>
-__device__ int exact_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& thr,
-                         float eps, const float* q, const DT* kb, int64_t kst, int64_t ksr, int R,
-                         int K, int u)
+// Exact rescoring of a row's c pool entries: pool[e].s becomes the exact score. The VEC
+// path keeps NBR key rows per lane in flight at once (the chains wait on one round trip per
+// batch) and walks the address dims in ascending order, one 8-dim chunk of q at a time, for
+// all NBR chains together.
+template <typename DT, bool VEC, int RP>
+__device__ void rescore_row(Entry* pool, int c, const float* q, const DT* kb, int64_t kst,
+                            int64_t ksr, int R, int u)
 {
-    constexpr int EPR = POOL / 16;
-    for (int e = u; e < c; e += 32) {   // two independent chains per iteration
-        const bool two = e + 16 < c;
-        const uint32_t j0 = pool[e].j;
-        const uint32_t j1 = two ? pool[e + 16].j : j0;
-        const float s0 = exact_score<DT, VEC, RP>(q, kb + int64_t(j0) * kst, ksr, R);
-        const float s1 = exact_score<DT, VEC, RP>(q, kb + int64_t(j1) * kst, ksr, R);
-        pool[e].s = s0;
-        if (two) pool[e + 16].s = s1;
+    if constexpr (VEC) {   // R == RP: every chunk lies inside the row
+        constexpr int NC = RP / 8;
+        constexpr int U4 = NC * (sizeof(DT) == 4 ? 2 : 1);   // 16-byte loads per key row
+        constexpr int NBR = U4 >= 16 ? 1 : 16 / U4;
+        for (int e0 = 0; e0 < c; e0 += 16 * NBR) {
+            uint4 lo[NBR][NC], hi[NBR][NC];
+#pragma unroll
+            for (int m = 0; m < NBR; ++m) {
+                const int e = e0 + u + 16 * m;
+                const uint32_t jr = pool[min(e, c - 1)].j;   // unconditional read: no LDS wait per entry
+                const uint32_t j = e < c ? jr : 0u;
+                const DT* krow = kb + int64_t(j) * kst;
+#pragma unroll
+                for (int cc = 0; cc < NC; ++cc) {
+                    lo[m][cc] = *reinterpret_cast<const uint4*>(krow + 8 * cc);
+                    if constexpr (sizeof(DT) == 4) hi[m][cc] = *reinterpret_cast<const uint4*>(krow + 8 * cc + 4);
+                    else hi[m][cc] = make_uint4(0, 0, 0, 0);
+                }
+            }
+            float acc[NBR];
+#pragma unroll
+            for (int m = 0; m < NBR; ++m) acc[m] = 0.0f;
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) {
+                const float4 qa = *reinterpret_cast<const float4*>(q + 8 * cc);
+                const float4 qb = *reinterpret_cast<const float4*>(q + 8 * cc + 4);
+#pragma unroll
+                for (int m = 0; m < NBR; ++m) {
+                    float kf[8];
+                    to_f32x8<DT>(lo[m][cc], hi[m][cc], kf);
+                    float a = acc[m];
+                    a = fmaf(qa.x, kf[0], a); a = fmaf(qa.y, kf[1], a);
+                    a = fmaf(qa.z, kf[2], a); a = fmaf(qa.w, kf[3], a);
+                    a = fmaf(qb.x, kf[4], a); a = fmaf(qb.y, kf[5], a);
+                    a = fmaf(qb.z, kf[6], a); a = fmaf(qb.w, kf[7], a);
+                    acc[m] = a;
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < NBR; ++m) {
+                const int e = e0 + u + 16 * m;
+                if (e < c) pool[e].s = acc[m];
+            }
+        }
+    } else {
+        for (int e = u; e < c; e += 32) {   // two independent chains per iteration
+            const bool two = e + 16 < c;
+            const uint32_t j0 = pool[e].j;
+            const uint32_t j1 = two ? pool[e + 16].j : j0;
+            const float s0 = exact_score<DT, VEC, RP>(q, kb + int64_t(j0) * kst, ksr, R);
+            const float s1 = exact_score<DT, VEC, RP>(q, kb + int64_t(j1) * kst, ksr, R);
+            pool[e].s = s0;
+            if (two) pool[e + 16].s = s1;
+        }
     }
+}
+
+// Exact selection of the min(K, c) best of a row's c exactly scored entries by (score desc,
+// index asc), radix-selected on the 64-bit keys (EPR >= ceil(c / 16) entries per lane); the
+// winners end up in pool[0..kept). Returns kept (uniform over the row); lane u == 0 stores
+// cnt and the exact threshold s_K - eps.
+template <int EPR>
+__device__ int select_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& thr, float eps,
+                          int K, int u)
+{
     uint64_t key[EPR];
 #pragma unroll
-    for (int m = 0; m < EPR; ++m) {
-        const int e = u + 16 * m;
-        key[m] = e < c ? make_key(pool[e].s, pool[e].j) : 0ull;   // real keys are > 0
+    for (int m = 0; m < EPR; ++m) {   // unconditional reads, masked: one LDS wait for the row
+        const uint2 en = reinterpret_cast<const uint2*>(pool)[u + 16 * m];
+        key[m] = u + 16 * m < c ? make_key(__uint_as_float(en.x), en.y) : 0ull;   // real keys are > 0
     }
     uint64_t prefix = 0, pmask = 0;
     if (c > K) {
@@ -396,11 +462,11 @@ __device__ int exact_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& th
             reinterpret_cast<uint4*>(hist)[2 * u] = make_uint4(0, 0, 0, 0);
             reinterpret_cast<uint4*>(hist)[2 * u + 1] = make_uint4(0, 0, 0, 0);
 #pragma unroll
-            for (int m = 0; m < EPR; ++m) {
-                if (u + 16 * m >= c || (key[m] & pmask) != prefix) continue;
+            for (int m = 0; m < EPR; ++m) {   // entries off the prefix count in a dummy bin
                 const uint32_t d = shift >= 0 ? uint32_t(key[m] >> shift) & 127u
                                               : uint32_t(key[m] << (-shift)) & 127u;
-                atomicAdd(&hist[d], 1u);
+                const bool in = u + 16 * m < c && (key[m] & pmask) == prefix;
+                atomicAdd(&hist[in ? d : uint32_t(kBins + u)], 1u);
             }
             int d, gt, eq;
             find_boundary(hist, u, need, d, gt, eq);
@@ -431,6 +497,20 @@ __device__ int exact_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& th
     return base;
 }
 
+// Exact rescoring of a row's c pool entries and exact selection of its min(K, c) best by
+// (score desc, index asc); the winners end up in pool[0..kept) with exact scores. Returns
+// kept (uniform over the row); lane u == 0 stores cnt and the exact threshold s_K - eps.
+template <typename DT, bool VEC, int RP, int POOL>
+__device__ int exact_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& thr,
+                         float eps, const float* q, const DT* kb, int64_t kst, int64_t ksr, int R,
+                         int K, int u)
+{
+    rescore_row<DT, VEC, RP>(pool, c, q, kb, kst, ksr, R, u);
+    constexpr int kSmall = 12;   // after a prune the pool rarely holds more than K + 64
+    if (c <= 16 * kSmall) return select_row<kSmall>(pool, hist, c, cnt, thr, eps, K, u);
+    return select_row<POOL / 16>(pool, hist, c, cnt, thr, eps, K, u);
+}
+
 // Sort row r's (exactly scored) winners into canonical order and write them plus pads.
 // `row` is the query position t in its batch; out_idx/out_scores point at the batch.
 template <int KP2, int POOL>
@@ -441,8 +521,9 @@ __device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
     uint64_t key[EPL];
 #pragma unroll
     for (int m = 0; m < EPL; ++m) {
-        const int i = u * EPL + m;
-        key[m] = i < kept ? make_key(pool[i].s, pool[i].j) : 0ull;
+        const int i = u * EPL + m;   // < KP2 < POOL: read unconditionally, masked
+        const uint2 en = reinterpret_cast<const uint2*>(pool)[i];
+        key[m] = i < kept ? make_key(__uint_as_float(en.x), en.y) : 0ull;
     }
 #pragma unroll
     for (int kk = 2; kk <= KP2; kk <<= 1) {
@@ -525,15 +606,16 @@ __global__ __launch_bounds__(kAbsmaxChunk) void key_absmax_kernel(TopkParams p)
 }
 
 template <typename DT, bool VEC, int RC, int KP2>
-__global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
+__device__ __forceinline__ void causal_topk_body(const TopkParams& p)
 {
     constexpr int RP = RC * 32;
-    // pool entries per row: two workgroups (<= 80 KiB of LDS each) per CU
-    constexpr int POOL = RP <= 64 ? 512 : 496;
+    // pool entries per row: two workgroups (<= 80 KiB of LDS each) per CU for RC <= 2; the
+    // wide variant runs one workgroup per CU (register-bound) and has LDS to spare
+    constexpr int POOL = 512;
     constexpr int LIMIT = POOL - kUnitMax;       // a pool above this is pruned at the next check
     constexpr int HEADROOM = 64;                 // a prune must leave this much room
     static_assert(LIMIT - HEADROOM > KP2 + 32, "pool too small for K");
-    static_assert(sizeof(TopkSmem<RP, POOL>) <= 80 * 1024, "two workgroups per CU");
+    static_assert(sizeof(TopkSmem<RP, POOL>) <= (RC <= 2 ? 80 : 160) * 1024, "LDS per workgroup");
     __shared__ TopkSmem<RP, POOL> sm;
 
     const int lane = lane_id();
@@ -624,13 +706,13 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
         }
     };
     // append the lane's candidates (keys jb .. jb+3 of row n) that reach the threshold; one
-    // LDS atomic reserves their slots, the others are written to the row's dummy slot POOL
+    // LDS atomic reserves their slots, the others are written to a dummy slot of the row
     auto append = [&](const f32x4_t& acc, const bool (&pp)[4], int jb) {
         const int cntp = int(pp[0]) + int(pp[1]) + int(pp[2]) + int(pp[3]);
         int pos = atomicAdd(&sm.cnt[n], cntp);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            sm.pool[n][pp[i] ? pos : POOL] = Entry{acc[i], uint32_t(jb + i)};
+            sm.pool[n][pp[i] ? pos : POOL + g] = Entry{acc[i], uint32_t(jb + i)};
             pos += int(pp[i]);
         }
     };
@@ -645,12 +727,15 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
         return acc;
     };
     // budget: 2-step units every wave may still take before a pool could overflow (a unit
-    // appends at most kUnitMax per row); equal in every wave, read after barriers
+    // appends at most kUnitMax per row). Every wave must take the same decisions at a check
+    // (the barriers must pair up), so they all decide on one snapshot of the counts: a second
+    // barrier keeps every wave from appending again until all of them have read it.
     int budget = max(1, (POOL - 0) / kUnitMax);
     auto check = [&]() {
-        __syncthreads();
-        const int cl = lane < kRows ? sm.cnt[lane] : 0;
-        if (__ballot(cl > LIMIT)) {   // same decision in every wave: all read after the barrier
+        __syncthreads();   // every append of the unit has landed
+        int cl = lane < kRows ? sm.cnt[lane] : 0;
+        __syncthreads();   // the snapshot is read in every wave before anyone appends again
+        if (__ballot(cl > LIMIT)) {
 #ifdef WF_TOPK_TIMING
             const uint64_t tc0 = wall_clock64();
 #endif
@@ -664,15 +749,16 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
                                                  sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
                                                  p.ksr, R, K, u);
             }
-            __syncthreads();
+            __syncthreads();   // every row is pruned
             th = row_ok ? sm.thr[n] : __builtin_inff();
+            cl = lane < kRows ? sm.cnt[lane] : 0;
+            __syncthreads();   // ... and read everywhere before anyone appends again
 #ifdef WF_TOPK_TIMING
             tcomp += wall_clock64() - tc0;
             ++ncomp;
 #endif
         }
-        const int cmax = __builtin_amdgcn_readfirstlane(
-            row_max16_i32(lane < kRows ? sm.cnt[lane] : 0));
+        const int cmax = __builtin_amdgcn_readfirstlane(row_max16_i32(cl));
         budget = max(1, (POOL - cmax) / kUnitMax);
     };
     if (iters > 0) {
@@ -726,17 +812,29 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 #ifdef WF_TOPK_TIMING
     uint64_t tm1 = wall_clock64();
 #endif
+#ifdef WF_TOPK_TIMING
+    uint64_t tmA = 0, tmB = 0;
+    int c_in = 0, c_pr = 0;
+#endif
     if (rr < kRows && r0 + rr < T) {
         int c = sm.cnt[rr];
+#ifdef WF_TOPK_TIMING
+        c_in = c;
+#endif
         if (c > K) {
             int c2 = c;
             prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
             c = c2;
         }
+#ifdef WF_TOPK_TIMING
+        tmA = wall_clock64();
+        c_pr = c;
+#endif
         const int kept = exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c, sm.cnt[rr],
                                                       sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
                                                       p.ksr, R, K, u);
 #ifdef WF_TOPK_TIMING
+        tmB = wall_clock64();
         emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, p.out_idx + b * T * p.k_eff,
                             nullptr, u);
 #else
@@ -745,21 +843,45 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_kernel(TopkParams p)
 #endif
     }
 #ifdef WF_TOPK_TIMING
+    const uint64_t tmC = wall_clock64();
     __syncthreads();
     if (threadIdx.x == 0 && p.out_scores) {
-        uint64_t* tm = reinterpret_cast<uint64_t*>(p.out_scores) + 4 * blockIdx.x;
+        uint64_t* tm = reinterpret_cast<uint64_t*>(p.out_scores) + 8 * blockIdx.x;
         tm[0] = tm0; tm[1] = tm1; tm[2] = wall_clock64(); tm[3] = uint64_t(rb) | (ncomp << 16) | (tcomp << 32);
+        tm[4] = tmA; tm[5] = tmB; tm[6] = tmC; tm[7] = uint64_t(c_in) | (uint64_t(c_pr) << 32);
     }
 #endif
+}
+
+// Two workgroups per CU: LDS (<= 80 KiB each) and registers (<= 256 per lane) both allow 2
+// waves per SIMD for address dims up to 64; the attribute keeps the register allocation
+// inside that bound. Wider addresses (RC = 4) keep their registers at 1 wave per SIMD.
+template <typename DT, bool VEC, int RC, int KP2>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
+void causal_topk_kernel(TopkParams p)
+{
+    causal_topk_body<DT, VEC, RC, KP2>(p);
+}
+template <typename DT, bool VEC, int RC, int KP2>
+__global__ __launch_bounds__(64 * kWaves) void causal_topk_wide_kernel(TopkParams p)
+{
+    causal_topk_body<DT, VEC, RC, KP2>(p);
+}
+
+template <typename DT, bool VEC, int RC, int KP2>
+void launch_topk_kp(const TopkParams& p, hipStream_t s)
+{
+    const dim3 grid(unsigned(p.B * p.n_row_blocks)), block(64 * kWaves);
+    if constexpr (RC <= 2) causal_topk_kernel<DT, VEC, RC, KP2><<<grid, block, 0, s>>>(p);
+    else causal_topk_wide_kernel<DT, VEC, RC, KP2><<<grid, block, 0, s>>>(p);
 }
 
 template <typename DT, bool VEC, int RC>
 hipError_t launch_topk_k(const TopkParams& p, hipStream_t s)
 {
-    const dim3 grid(unsigned(p.B * p.n_row_blocks)), block(64 * kWaves);
-    if (p.k_eff <= 64) causal_topk_kernel<DT, VEC, RC, 64><<<grid, block, 0, s>>>(p);
-    else if (p.k_eff <= 128) causal_topk_kernel<DT, VEC, RC, 128><<<grid, block, 0, s>>>(p);
-    else causal_topk_kernel<DT, VEC, RC, 256><<<grid, block, 0, s>>>(p);
+    if (p.k_eff <= 64) launch_topk_kp<DT, VEC, RC, 64>(p, s);
+    else if (p.k_eff <= 128) launch_topk_kp<DT, VEC, RC, 128>(p, s);
+    else launch_topk_kp<DT, VEC, RC, 256>(p, s);
     return hipGetLastError();
 }
 
