@@ -1,5 +1,6 @@
 """Per-token learned address vectors (mirrors routing_attention/models/learned_address.py
-of the reference: LearnedAddressModule, same parameters and state_dict keys)."""
+of the reference: LearnedAddressModule, PerLayerAddressBook and the config helpers, same
+parameters and state_dict keys)."""
 
 from __future__ import annotations
 
@@ -42,3 +43,62 @@ class LearnedAddressModule(nn.Module):
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
         q, _ = self.forward_query_key(hidden)
         return q
+
+    def retrieval_scores(self, hidden: torch.Tensor) -> torch.Tensor:
+        """Dense (B, T, T) address similarity (reference learned_address.py:53-56). The
+        retrieval itself never builds this matrix; Recall@K can use
+        ``routing_attention.evaluation.recall.compute_recall_from_addresses`` instead."""
+        q, k = self.forward_query_key(hidden)
+        return torch.matmul(q, k.transpose(-2, -1))
+
+
+class PerLayerAddressBook(nn.Module):
+    """One LearnedAddressModule per transformer layer (reference learned_address.py:59-90)."""
+
+    def __init__(
+        self,
+        n_layers: int,
+        d_model: int,
+        address_dim: int = 32,
+        similarity: Literal["symmetric", "asymmetric"] = "asymmetric",
+        normalize: bool = True,
+    ):
+        super().__init__()
+        self.n_layers = n_layers
+        self.addresses = nn.ModuleList([
+            LearnedAddressModule(d_model=d_model, address_dim=address_dim, similarity=similarity,
+                                 normalize=normalize)
+            for _ in range(n_layers)
+        ])
+
+    def get_address(self, layer_idx: int) -> LearnedAddressModule:
+        return self.addresses[layer_idx]
+
+    def get_router(self, layer_idx: int) -> LearnedAddressModule:
+        return self.get_address(layer_idx)
+
+    def retrieval_scores(self, hidden: torch.Tensor, layer_idx: int) -> torch.Tensor:
+        return self.get_address(layer_idx).retrieval_scores(hidden)
+
+
+def build_address_book_from_config(config: dict) -> PerLayerAddressBook:
+    """Address book from the ``learned_address`` and ``model`` config sections (reference
+    learned_address.py:93-103)."""
+    la_cfg = config.get("learned_address", {})
+    model_cfg = config["model"]
+    return PerLayerAddressBook(
+        n_layers=model_cfg["n_layers"],
+        d_model=model_cfg["d_model"],
+        address_dim=la_cfg.get("address_dim", la_cfg.get("routing_dim", 32)),
+        similarity=la_cfg.get("similarity", "asymmetric"),
+        normalize=la_cfg.get("normalize", True),
+    )
+
+
+def attach_address_book_to_model(model: nn.Module, address_book: PerLayerAddressBook) -> None:
+    """Point every attention layer of a TransformerLM at its address module (reference
+    learned_address.py:106-112)."""
+    model.address_book = address_book
+    for layer_idx, block in enumerate(model.blocks):
+        if hasattr(block.attn, "set_address_module"):
+            block.attn.set_address_module(address_book.get_address(layer_idx))
