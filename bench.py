@@ -165,6 +165,18 @@ def run_leg(args, dev, K, scale, readout_bytes):
         print(json.dumps({"leg": "topk", "ms": round(ms, 4)}), flush=True)
         return
     idx = causal_topk(dev["qa"], dev["ka"], K)
+    if args.leg == "backward":
+        from routing_attention.kernels.sparse_autograd import readout_bwd, readout_fwd_lse
+
+        out, lse2 = readout_fwd_lse(dev["q"], dev["k"], dev["v"], idx, scale)
+        dout = torch.randn_like(out)
+        fn = lambda: readout_bwd(dev["q"], dev["k"], dev["v"], idx, lse2, dout, scale)  # noqa: E731
+        ms = time_loop(fn, args.steps, args.warmup)
+        fwd_ms = time_loop(lambda: readout_fwd_lse(dev["q"], dev["k"], dev["v"], idx, scale),
+                           args.steps, args.warmup)
+        print(json.dumps({"leg": "backward", "ms": round(ms, 4), "fwd_lse_ms": round(fwd_ms, 4),
+                          "gathered_gbs": round(2 * (readout_bytes) / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return
     fn = lambda: sparse_meat_attention(dev["q"], dev["k"], dev["v"], idx, scale)  # noqa: E731
     ms = time_loop(fn, args.steps, args.warmup)
     print(json.dumps({"leg": "readout", "ms": round(ms, 4),
@@ -238,7 +250,7 @@ def main():
                     help="c4 (default) is the metric's workload; c2 times the 4-layer decoder")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
-    ap.add_argument("--leg", default="all", choices=["all", "topk", "readout", "copy"],
+    ap.add_argument("--leg", default="all", choices=["all", "topk", "readout", "backward", "copy"],
                     help="profiling aid: run only one kernel (or a 256 MiB device copy used to "
                          "calibrate the FETCH_SIZE / WRITE_SIZE counters) and print its timing")
     args = ap.parse_args()

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define WF_ABI_VERSION 1
+#define WF_ABI_VERSION 2
 
 typedef enum wf_status {
     WF_OK = 0,
@@ -105,6 +105,69 @@ int wf_sparse_readout_fwd(const void* q, const void* k, const void* v, int dtype
                           const int32_t* indices, const int64_t* idx_strides, int64_t K,
                           float scale, unsigned flags,
                           void* out, const int64_t* out_strides, void* stream);
+
+/*
+ * wf_sparse_readout_fwd that also writes the softmax normaliser the backward needs.
+ * Replaces: the forward half of the reference's differentiable readout (attention.py:35-55,
+ *           whose gather formulation autograd differentiates).
+ * lse2 : (B, H, T) float32, contiguous: log2 of the softmax denominator of every row in
+ *        the base-2 domain, lse2 = log2(sum_s 2^(log2(e) * scale * q.k_s)) = lse * log2(e).
+ * Other arguments and limits as wf_sparse_readout_fwd.
+ */
+int wf_sparse_readout_fwd_lse(const void* q, const void* k, const void* v, int dtype,
+                              int64_t B, int64_t H, int64_t T, int64_t D,
+                              const int64_t* q_strides, const int64_t* k_strides,
+                              const int64_t* v_strides,
+                              const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                              float scale, unsigned flags,
+                              void* out, const int64_t* out_strides, float* lse2, void* stream);
+
+/* Arguments of the readout backward. */
+typedef struct wf_readout_bwd_args {
+    const void* q;              /* (B, H, T, D) forward inputs, strides *_strides  */
+    const void* k;
+    const void* v;
+    const void* dout;           /* (B, H, T, D) gradient of the forward output      */
+    const int32_t* indices;     /* (B, T, K) int32, idx_strides[2] == 1             */
+    const float* lse2;          /* (B, H, T) from wf_sparse_readout_fwd_lse         */
+    void* dq;                   /* (B, H, T, D) outputs, every element written      */
+    void* dk;
+    void* dv;
+    void* workspace;            /* >= wf_sparse_readout_bwd_workspace_bytes(...)    */
+    size_t workspace_bytes;
+    int64_t q_strides[4];
+    int64_t k_strides[4];
+    int64_t v_strides[4];
+    int64_t dout_strides[4];
+    int64_t dq_strides[4];
+    int64_t dk_strides[4];
+    int64_t dv_strides[4];
+    int64_t idx_strides[3];
+    int64_t B, H, T, D, K;
+    int dtype;                  /* wf_dtype of every (B, H, T, D) tensor */
+    float scale;
+    unsigned flags;             /* WF_FLAG_MASK_PADS as in the forward   */
+} wf_readout_bwd_args;
+
+/* Device workspace of wf_sparse_readout_bwd for this shape (0 and wf_last_error() set if it
+ * cannot be sized, e.g. no device). */
+size_t wf_sparse_readout_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K);
+
+/*
+ * Backward of the sparse readout with the indices held fixed.
+ * Replaces: the autograd backward of the reference's differentiable readout
+ *           (attention.py:35-55, _gather_kv_heads :58-69): dq, and dk/dv accumulated over
+ *           every (row, slot) that selected a key (duplicates counted per slot).
+ * With p the forward's softmax weights, dp_s = dout . v_s, delta = sum_s p_s dp_s:
+ *   dq_t = scale sum_s p_s (dp_s - delta) k_s,  dk_j = scale sum p_s (dp_s - delta_t) q_t,
+ *   dv_j = sum p_s dout_t   (sums over the (t, s) with index j for dk, dv).
+ * fp32 accumulation, deterministic (no floating-point atomics), one rounding per element.
+ * Layout: every (B, H, T, D) tensor with contiguous head dim, 16-byte aligned rows and a
+ * per-(b, h) span below 4 GiB (the (B, T, H, D) memory of the module qualifies);
+ * otherwise WF_ERR_UNSUPPORTED. Limits: D in {32, 64, 128}, 1 <= K <= 1024,
+ * B*T*K < 2^32.
+ */
+int wf_sparse_readout_bwd(const wf_readout_bwd_args* args, void* stream);
 
 /* Arguments of the fused forward, one struct so the entry point stays stable. */
 typedef struct wf_fused_args {

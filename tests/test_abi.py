@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.wf_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.wf_abi_version() == _lib.ABI_VERSION == 2
 
 
 def _i64(*v):
@@ -144,3 +144,52 @@ def test_status_maps_to_reference_exception_types():
     with pytest.raises(_lib.WayfinderHipError):
         _lib.check(_lib.WF_ERR_HIP)
     _lib.check(_lib.WF_OK)
+
+
+def _bwd(lib, **kw):
+    B, H, T, D, K = 1, 2, 64, 64, 8
+    st = (H * T * D, D, H * D, 1)          # (B, T, H, D) memory viewed as (B, H, T, D)
+    a = _lib.ReadoutBwdArgs()
+    a.q = a.k = a.v = a.dout = a.dq = a.dk = a.dv = FAKE
+    a.indices = a.lse2 = a.workspace = FAKE
+    a.workspace_bytes = 1 << 30
+    for f in ("q", "k", "v", "dout", "dq", "dk", "dv"):
+        getattr(a, f + "_strides")[:] = list(st)
+    a.idx_strides[:] = [T * K, K, 1]
+    a.B, a.H, a.T, a.D, a.K = B, H, T, D, K
+    a.dtype, a.scale, a.flags = 2, 0.125, 0
+    for k, v in kw.items():
+        if k.endswith("_strides"):
+            getattr(a, k)[:] = list(v)
+        else:
+            setattr(a, k, v)
+    return lib.wf_sparse_readout_bwd(ctypes.byref(a), None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=7), _lib.WF_ERR_UNSUPPORTED, "dtype"),
+    (dict(D=48), _lib.WF_ERR_UNSUPPORTED, "head_dim"),
+    (dict(K=0), _lib.WF_ERR_INVALID_ARGUMENT, "K must be"),
+    (dict(K=2000), _lib.WF_ERR_UNSUPPORTED, "K=2000"),
+    (dict(dout=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(dk=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(lse2=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(q_strides=(2 * 64 * 64, 64, 128, 2)), _lib.WF_ERR_UNSUPPORTED, "contiguous head dim"),
+    (dict(dv=FAKE + 2), _lib.WF_ERR_UNSUPPORTED, "16-byte"),
+    (dict(idx_strides=(64 * 8, 8, 2)), _lib.WF_ERR_UNSUPPORTED, "index rows"),
+])
+def test_readout_bwd_contract_errors(lib, kw, code, msg):
+    assert _bwd(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_readout_bwd_empty_is_noop(lib):
+    assert _bwd(lib, T=0) == _lib.WF_OK
+    assert _bwd(lib, B=0) == _lib.WF_OK
+
+
+def test_readout_fwd_lse_needs_lse(lib):
+    st = _i64(2 * 64 * 64, 64, 128, 1)
+    rc = lib.wf_sparse_readout_fwd_lse(FAKE, FAKE, FAKE, 2, 1, 2, 64, 64, st, st, st, FAKE,
+                                       _i64(64 * 8, 8, 1), 8, 0.125, 0, FAKE, st, None, None)
+    assert rc == _lib.WF_ERR_INVALID_ARGUMENT and "lse2" in _lib.last_error()

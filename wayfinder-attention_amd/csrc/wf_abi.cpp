@@ -140,11 +140,11 @@ int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T
 int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
                 int64_t T, int64_t D, const int64_t* qs, const int64_t* ks, const int64_t* vs,
                 const int32_t* idx, const int64_t* is, int64_t K, float scale, unsigned flags,
-                void* out, const int64_t* os, hipStream_t stream)
+                void* out, const int64_t* os, float* lse2, hipStream_t stream)
 {
     if (B * H * T == 0) return WF_OK;
     wf::ReadoutParams p{};
-    p.q = q; p.k = k; p.v = v; p.out = out; p.idx = idx;
+    p.q = q; p.k = k; p.v = v; p.out = out; p.idx = idx; p.lse2 = lse2;
     for (int i = 0; i < 4; ++i) { p.qs[i] = qs[i]; p.ks[i] = ks[i]; p.vs[i] = vs[i]; p.os[i] = os[i]; }
     for (int i = 0; i < 3; ++i) p.is[i] = is[i];
     p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
@@ -216,8 +216,92 @@ int wf_sparse_readout_fwd(const void* q, const void* k, const void* v, int dtype
                            idx_strides, K, out, out_strides);
     if (rc != WF_OK) return rc;
     rc = run_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
-                     idx_strides, K, scale, flags, out, out_strides, static_cast<hipStream_t>(stream));
+                     idx_strides, K, scale, flags, out, out_strides, nullptr,
+                     static_cast<hipStream_t>(stream));
     return rc == WF_OK ? ok() : rc;
+}
+
+int wf_sparse_readout_fwd_lse(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                              int64_t H, int64_t T, int64_t D, const int64_t* q_strides,
+                              const int64_t* k_strides, const int64_t* v_strides,
+                              const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                              float scale, unsigned flags, void* out, const int64_t* out_strides,
+                              float* lse2, void* stream)
+{
+    int rc = check_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
+                           idx_strides, K, out, out_strides);
+    if (rc != WF_OK) return rc;
+    if (!lse2 && B * H * T > 0) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_fwd_lse: NULL lse2");
+    rc = run_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
+                     idx_strides, K, scale, flags, out, out_strides, lse2,
+                     static_cast<hipStream_t>(stream));
+    return rc == WF_OK ? ok() : rc;
+}
+
+size_t wf_sparse_readout_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K)
+{
+    if (B <= 0 || H <= 0 || T <= 0 || K <= 0) return 0;
+    hipError_t e = hipSuccess;
+    const size_t n = wf::sparse_readout_bwd_workspace(B, H, T, K, &e);
+    if (e != hipSuccess) fail(WF_ERR_HIP, "sparse_readout_bwd: workspace sizing: %s", hipGetErrorString(e));
+    return n;
+}
+
+int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
+{
+    if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: NULL argument struct");
+    int rc = check_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
+                           a->k_strides, a->v_strides, a->indices, a->idx_strides, a->K, a->dout,
+                           a->dout_strides);
+    if (rc != WF_OK) return rc;
+    const int64_t B = a->B, H = a->H, T = a->T, D = a->D, K = a->K;
+    if (B * H * T == 0) return ok();
+    if (!a->dq || !a->dk || !a->dv || !a->lse2)
+        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: NULL dq/dk/dv/lse2 pointer");
+    if (B * T * K >= (int64_t(1) << 32) - 1 || B * T >= (int64_t(1) << 32) - 1)
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: B*T*K=%lld exceeds 32-bit list offsets", (long long)(B * T * K));
+    const int dt = a->dtype;
+    const int64_t es = int64_t(elem_size(dt));
+    auto fast_ok = [&](const void* base, const int64_t* st) {
+        return vec_ok(base, dt, st, 4, D) && st[2] >= 0 && (T - 1) * st[2] * es + D * es < (int64_t(1) << 32);
+    };
+    if (!(fast_ok(a->q, a->q_strides) && fast_ok(a->k, a->k_strides) && fast_ok(a->v, a->v_strides) &&
+          fast_ok(a->dout, a->dout_strides) && fast_ok(a->dq, a->dq_strides) &&
+          fast_ok(a->dk, a->dk_strides) && fast_ok(a->dv, a->dv_strides)))
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: every (B,H,T,D) tensor needs a contiguous head dim, "
+                                        "16-byte aligned rows and a per-(b,h) span below 4 GiB");
+    if (a->idx_strides[2] != 1)
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: index rows must be contiguous (idx_strides[2] == 1)");
+    hipError_t e = hipSuccess;
+    const size_t need = wf::sparse_readout_bwd_workspace(B, H, T, K, &e);
+    if (e != hipSuccess) return hip_fail("sparse_readout_bwd: workspace sizing", e);
+    if (!a->workspace || a->workspace_bytes < need)
+        return fail(WF_ERR_WORKSPACE, "sparse_readout_bwd: workspace of %zu bytes required, got %zu", need,
+                    a->workspace ? a->workspace_bytes : size_t(0));
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0)
+        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: workspace not 256-byte aligned");
+    wf::ReadoutBwdParams p{};
+    p.q = a->q; p.k = a->k; p.v = a->v; p.dout = a->dout;
+    p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
+    p.idx = a->indices; p.lse2 = a->lse2;
+    for (int i = 0; i < 4; ++i) {
+        p.qs[i] = a->q_strides[i]; p.ks[i] = a->k_strides[i]; p.vs[i] = a->v_strides[i];
+        p.gs[i] = a->dout_strides[i]; p.dqs[i] = a->dq_strides[i]; p.dks[i] = a->dk_strides[i];
+        p.dvs[i] = a->dv_strides[i];
+    }
+    for (int i = 0; i < 3; ++i) p.is[i] = a->idx_strides[i];
+    p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
+    p.scale = a->scale; p.flags = a->flags;
+    const int64_t nbh = B * H;
+    p.seg_per_pair = 8 / gcd64(nbh, 8);
+    p.rows_per_seg = cdiv(T, p.seg_per_pair);
+    p.vpairs = nbh * p.seg_per_pair;
+    p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
+    if (p.vpairs * p.wg_per_vpair >= (int64_t(1) << 31))
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: problem too large for one launch");
+    e = wf::launch_sparse_readout_bwd(dt, p, a->workspace, a->workspace_bytes, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("sparse_readout_bwd: launch", e);
+    return ok();
 }
 
 int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
@@ -241,7 +325,7 @@ int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
     if (rc != WF_OK) return rc;
     rc = run_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
                      a->k_strides, a->v_strides, a->out_idx, is, k_eff, a->scale, a->flags,
-                     a->out, a->out_strides, s);
+                     a->out, a->out_strides, nullptr, s);
     return rc == WF_OK ? ok() : rc;
 }
 

@@ -120,10 +120,35 @@ struct ReadoutParams {
     int64_t B, H, T, D, K;
     float scale;
     unsigned flags;
+    float* lse2;            // optional (B, H, T) contiguous: log2 of the softmax denominator
+                            // in the kernels' base-2 domain (see wf_sparse_readout_fwd_lse)
     int64_t seg_per_pair;   // row segments per (b,h) pair (XCD balance)
     int64_t rows_per_seg;
     int64_t vpairs;         // B*H*seg_per_pair virtual pairs
     int64_t wg_per_vpair;   // workgroups per virtual pair
+};
+
+// Backward of the readout (fixed indices). Both passes use the forward's XCD-aware mapping:
+// the row pass over query rows t, the key pass over key rows j, of one (b, h) pair per XCD.
+struct ReadoutBwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* dout;
+    void* dq;
+    void* dk;
+    void* dv;
+    const int32_t* idx;
+    const float* lse2;       // (B, H, T) from the forward
+    float* delta;            // (B, H, T) workspace: sum_s p_s (dout . v_s), row pass -> key pass
+    const uint32_t* off;     // (B*T + 1) start of each key's list in `rows`
+    const uint32_t* rows;    // query rows t referencing each key, grouped by key, t ascending
+    int64_t qs[4], ks[4], vs[4], gs[4], dqs[4], dks[4], dvs[4];  // element strides (B, H, T, D)
+    int64_t is[3];
+    int64_t B, H, T, D, K;
+    float scale;
+    unsigned flags;
+    int64_t seg_per_pair, rows_per_seg, vpairs, wg_per_vpair;   // as in ReadoutParams
 };
 
 // Key-magnitude chunk size of the screening bound (keys per chunk).
@@ -135,5 +160,9 @@ constexpr int kReadoutRowsPerWG = 16;
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutParams& p, hipStream_t s);
+// device workspace of the backward for this shape (index transpose, per-row deltas and the
+// rocPRIM scan / sort scratch); 0 with *err set when rocPRIM cannot size it
+size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K, hipError_t* err);
+hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s);
 
 }  // namespace wf

@@ -1,0 +1,361 @@
+// wf_readout_bwd.hip -- backward of the sparse readout with fixed indices (gfx950).
+//
+// Counterpart of the autograd the reference gets from its differentiable readout
+// (routing_attention/models/attention.py:35-55 with _gather_kv_heads :58-69: gather,
+// softmax, weighted sum), whose backward scatters (B, H, T, K, D) gradient copies back into
+// k and v with index_put accumulation. With p_s the softmax weight of slot s of row t,
+// dp_s = dout_t . v_{j_s} and delta_t = sum_s p_s dp_s:
+//
+//   dq_t = scale * (sum_s p_s dp_s k_{j_s} - delta_t * sum_s p_s k_{j_s})
+//   dk_j = scale * sum_{(t,s): j_s = j} p_s (dp_s - delta_t) q_t
+//   dv_j = sum_{(t,s): j_s = j} p_s dout_t
+//
+// computed without floating-point atomics, so the gradients are deterministic:
+//  1. index transpose: a counting pass and an exclusive scan give each key j its list
+//     offset; a stable rocPRIM radix sort of (b*T + j) keys with the query row t as value
+//     fills the lists, t ascending. Masked pad slots sort past the last list.
+//  2. row pass (the forward's mapping: one wave walks 4 query rows, D/8 lanes per
+//     neighbour): recomputes p from the forward's base-2 log-sum-exp and writes dq and
+//     delta (exact, from the row's own p and dp rather than the rounded output);
+//  3. key pass (same mapping over key rows): each key row walks its list, gathering q_t and
+//     dout_t -- the forward's access pattern with the roles of query and key swapped -- and
+//     recomputes p and dp for every entry. Nothing of size (B, H, T, K) is stored.
+// All accumulation is fp32; each gradient element is rounded once to the input dtype.
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
+
+#include "wf_readout_dev.h"
+
+namespace wf {
+namespace {
+
+__global__ void fill_u32(uint32_t* p, int64_t n, uint32_t v)
+{
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// One thread per (b, t, s) slot: key b*T + j (j wrapped and clamped as in the forward),
+// value t. Masked pad slots (s > t on rows t < K-1 with WF_FLAG_MASK_PADS) carry no weight:
+// they get the key B*T, past every list, and are not counted.
+__global__ void bwd_transpose_keys(const int32_t* idx, int64_t is0, int64_t is1, int64_t is2,
+                                   int64_t B, int64_t T, int64_t K, bool mask_pads,
+                                   uint32_t* keys, uint32_t* vals, uint32_t* counts)
+{
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= B * T * K) return;
+    const int64_t b = e / (T * K);
+    const int64_t r = e - b * T * K;
+    const int64_t t = r / K;
+    const int64_t s = r - t * K;
+    int64_t j = idx[b * is0 + t * is1 + s * is2];
+    if (j < 0) j += T;
+    j = j < 0 ? 0 : (j > T - 1 ? T - 1 : j);
+    const bool masked = mask_pads && t < K - 1 && s > t;
+    const uint32_t key = masked ? uint32_t(B * T) : uint32_t(b * T + j);
+    keys[e] = key;
+    vals[e] = uint32_t(t);
+    if (!masked) atomicAdd(&counts[key], 1u);
+}
+
+struct Pair { int64_t b, h, r0; int n; };
+
+// The forward's XCD-aware mapping: returns the (b, h) pair and the first of this wave's
+// (up to kRowsPerWave) consecutive rows; n = 0 when the wave has no rows.
+__device__ __forceinline__ Pair map_rows(const ReadoutBwdParams& p, int wave)
+{
+    Pair r{0, 0, 0, 0};
+    const int64_t xcd = blockIdx.x & 7;
+    const int64_t it = blockIdx.x >> 3;
+    const int64_t vp = (it / p.wg_per_vpair) * 8 + xcd;
+    if (vp >= p.vpairs) return r;
+    const int64_t chunk = it % p.wg_per_vpair;
+    const int64_t pair = vp / p.seg_per_pair;
+    const int64_t seg = vp % p.seg_per_pair;
+    r.b = pair / p.H;
+    r.h = pair % p.H;
+    const int64_t t0 = seg * p.rows_per_seg;
+    const int64_t t1 = min(p.T, t0 + p.rows_per_seg);
+    r.r0 = t0 + (chunk * kWaves + wave) * kRowsPerWave;
+    if (r.r0 < t1) r.n = int(min(int64_t(kRowsPerWave), t1 - r.r0));
+    return r;
+}
+
+__device__ __forceinline__ int wrap_index(int j, int T)
+{
+    j += (j >> 31) & T;
+    return min(max(j, 0), T - 1);
+}
+
+// Row pass: dq and delta for query rows t of one (b, h) pair.
+template <typename DT, int D>
+__global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams p)
+{
+    constexpr int LPN = D / 8;
+    constexpr int NPS = 64 / LPN;
+    constexpr uint32_t ES = sizeof(DT);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sub = lane % LPN;
+    const int grp = lane / LPN;
+    const Pair w = map_rows(p, wave);
+    if (w.n == 0) return;
+    const int64_t b = w.b, h = w.h, tw = w.r0;
+    const int K = int(p.K);
+    const int T = int(p.T);
+    const bool mask_flag = (p.flags & 1u) != 0;
+    const float sl2 = p.scale * kLog2e;
+
+    const char* kb = reinterpret_cast<const char*>(static_cast<const DT*>(p.k) + b * p.ks[0] + h * p.ks[1]);
+    const char* vb = reinterpret_cast<const char*>(static_cast<const DT*>(p.v) + b * p.vs[0] + h * p.vs[1]);
+    const char* qb = reinterpret_cast<const char*>(static_cast<const DT*>(p.q) + b * p.qs[0] + h * p.qs[1] + tw * p.qs[2]);
+    const char* gb = reinterpret_cast<const char*>(static_cast<const DT*>(p.dout) + b * p.gs[0] + h * p.gs[1] + tw * p.gs[2]);
+    char* db = reinterpret_cast<char*>(static_cast<DT*>(p.dq) + b * p.dqs[0] + h * p.dqs[1] + tw * p.dqs[2]);
+    const uint32_t krow = uint32_t(p.ks[2]) * ES, vrow = uint32_t(p.vs[2]) * ES;
+    const uint32_t qrow = uint32_t(p.qs[2]) * ES, grow = uint32_t(p.gs[2]) * ES;
+    const uint32_t drow = uint32_t(p.dqs[2]) * ES;
+    const uint32_t loff = uint32_t(sub) * 8u * ES;
+    const int32_t* ib = p.idx + b * p.is[0] + tw * p.is[1];
+    const int64_t rbase = (b * p.H + h) * p.T + tw;
+
+    for (int r = 0; r < w.n; ++r) {
+        const int t = int(tw) + r;
+        uint4 qlo, qhi, glo, ghi;
+        ld16<DT>(qb, uint32_t(r) * qrow + loff, qlo, qhi);
+        ld16<DT>(gb, uint32_t(r) * grow + loff, glo, ghi);
+        const float lt2 = p.lse2[rbase + r];
+        const int lim = (mask_flag && t < K - 1) ? t + 1 : K;   // slots >= lim carry no weight
+        const int32_t* ip = ib + r * p.is[1];
+        float A[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float Bk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float dsum = 0.0f;
+        for (int s0 = 0; s0 < K; s0 += 2 * NPS) {
+            const int sl[2] = {s0 + grp, s0 + NPS + grp};
+            uint4 klo[2], khi[2], vlo[2], vhi[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int j = wrap_index(ip[min(sl[u], K - 1)], T);
+                ld16<DT>(kb, uint32_t(j) * krow + loff, klo[u], khi[u]);
+                ld16<DT>(vb, uint32_t(j) * vrow + loff, vlo[u], vhi[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
+                const float dp = group_sum<LPN>(dot8<DT>(glo, ghi, vlo[u], vhi[u]));
+                const float pu = sl[u] < lim ? exp2f(d * sl2 - lt2) : 0.0f;
+                const float pd = pu * dp;
+                dsum += pd;
+                float kf[8];
+                cvt8<DT>(klo[u], khi[u], kf);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    A[e] = fmaf(pd, kf[e], A[e]);
+                    Bk[e] = fmaf(pu, kf[e], Bk[e]);
+                }
+            }
+        }
+        const float delta = group_allreduce<LPN, false>(dsum);
+        float o8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float a = group_allreduce<LPN, false>(A[e]);
+            const float bk = group_allreduce<LPN, false>(Bk[e]);
+            o8[e] = p.scale * (a - delta * bk);
+        }
+        if (grp == 0) {
+            store_row8<DT, true>(reinterpret_cast<DT*>(db + uint32_t(r) * drow + loff), 1, o8);
+            if (sub == 0) p.delta[rbase + r] = delta;
+        }
+    }
+}
+
+// Key pass: dk and dv for key rows j of one (b, h) pair.
+template <typename DT, int D>
+__global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams p)
+{
+    constexpr int LPN = D / 8;
+    constexpr int NPS = 64 / LPN;
+    constexpr uint32_t ES = sizeof(DT);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sub = lane % LPN;
+    const int grp = lane / LPN;
+    const Pair w = map_rows(p, wave);
+    if (w.n == 0) return;
+    const int64_t b = w.b, h = w.h, jw = w.r0;
+    const float sl2 = p.scale * kLog2e;
+
+    const char* qb = reinterpret_cast<const char*>(static_cast<const DT*>(p.q) + b * p.qs[0] + h * p.qs[1]);
+    const char* gb = reinterpret_cast<const char*>(static_cast<const DT*>(p.dout) + b * p.gs[0] + h * p.gs[1]);
+    const char* kb = reinterpret_cast<const char*>(static_cast<const DT*>(p.k) + b * p.ks[0] + h * p.ks[1] + jw * p.ks[2]);
+    const char* vb = reinterpret_cast<const char*>(static_cast<const DT*>(p.v) + b * p.vs[0] + h * p.vs[1] + jw * p.vs[2]);
+    char* dkb = reinterpret_cast<char*>(static_cast<DT*>(p.dk) + b * p.dks[0] + h * p.dks[1] + jw * p.dks[2]);
+    char* dvb = reinterpret_cast<char*>(static_cast<DT*>(p.dv) + b * p.dvs[0] + h * p.dvs[1] + jw * p.dvs[2]);
+    const uint32_t qrow = uint32_t(p.qs[2]) * ES, grow = uint32_t(p.gs[2]) * ES;
+    const uint32_t krow = uint32_t(p.ks[2]) * ES, vrow = uint32_t(p.vs[2]) * ES;
+    const uint32_t dkrow = uint32_t(p.dks[2]) * ES, dvrow = uint32_t(p.dvs[2]) * ES;
+    const uint32_t loff = uint32_t(sub) * 8u * ES;
+    const float* lse = p.lse2 + (b * p.H + h) * p.T;
+    const float* dl = p.delta + (b * p.H + h) * p.T;
+    const uint32_t* off = p.off + b * p.T + jw;
+
+    for (int r = 0; r < w.n; ++r) {
+        uint4 klo, khi, vlo, vhi;
+        ld16<DT>(kb, uint32_t(r) * krow + loff, klo, khi);
+        ld16<DT>(vb, uint32_t(r) * vrow + loff, vlo, vhi);
+        const uint32_t e0 = off[r], e1 = off[r + 1];
+        float ak[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float av[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t e = e0; e < e1; e += 2 * NPS) {
+            const uint32_t en[2] = {e + uint32_t(grp), e + uint32_t(NPS + grp)};
+            int t[2];
+            uint4 qlo[2], qhi[2], glo[2], ghi[2];
+            float lt2[2], dlt[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                t[u] = en[u] < e1 ? int(p.rows[en[u]]) : 0;
+                ld16<DT>(qb, uint32_t(t[u]) * qrow + loff, qlo[u], qhi[u]);
+                ld16<DT>(gb, uint32_t(t[u]) * grow + loff, glo[u], ghi[u]);
+                lt2[u] = lse[t[u]];
+                dlt[u] = dl[t[u]];
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float d = group_sum<LPN>(dot8<DT>(qlo[u], qhi[u], klo, khi));
+                const float dp = group_sum<LPN>(dot8<DT>(glo[u], ghi[u], vlo, vhi));
+                const float pu = en[u] < e1 ? exp2f(d * sl2 - lt2[u]) : 0.0f;
+                const float ds = pu * (dp - dlt[u]);
+                float qf[8], gf[8];
+                cvt8<DT>(qlo[u], qhi[u], qf);
+                cvt8<DT>(glo[u], ghi[u], gf);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    ak[c] = fmaf(ds, qf[c], ak[c]);
+                    av[c] = fmaf(pu, gf[c], av[c]);
+                }
+            }
+        }
+        float ok8[8], ov8[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            ok8[c] = p.scale * group_allreduce<LPN, false>(ak[c]);
+            ov8[c] = group_allreduce<LPN, false>(av[c]);
+        }
+        if (grp == 0) {
+            store_row8<DT, true>(reinterpret_cast<DT*>(dkb + uint32_t(r) * dkrow + loff), 1, ok8);
+            store_row8<DT, true>(reinterpret_cast<DT*>(dvb + uint32_t(r) * dvrow + loff), 1, ov8);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- workspace layout
+size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int key_bits(int64_t B, int64_t T)
+{
+    int bits = 1;
+    while ((int64_t(1) << bits) <= B * T) ++bits;   // keys take values 0 .. B*T
+    return bits;
+}
+
+struct BwdLayout {
+    size_t counts, off, keys, keys_out, vals, vals_out, delta, scan_tmp, sort_tmp, total;
+    size_t scan_bytes, sort_bytes;
+};
+
+hipError_t bwd_layout(int64_t B, int64_t H, int64_t T, int64_t K, BwdLayout& L)
+{
+    const size_t nkeys = size_t(B * T) + 1;
+    const size_t n = size_t(B * T * K);
+    L.scan_bytes = 0;
+    L.sort_bytes = 0;
+    hipError_t e = rocprim::exclusive_scan(nullptr, L.scan_bytes, static_cast<const uint32_t*>(nullptr),
+                                           static_cast<uint32_t*>(nullptr), 0u, nkeys,
+                                           rocprim::plus<uint32_t>(), hipStream_t(0));
+    if (e != hipSuccess) return e;
+    e = rocprim::radix_sort_pairs(nullptr, L.sort_bytes, static_cast<const uint32_t*>(nullptr),
+                                  static_cast<uint32_t*>(nullptr), static_cast<const uint32_t*>(nullptr),
+                                  static_cast<uint32_t*>(nullptr), n, 0, key_bits(B, T), hipStream_t(0));
+    if (e != hipSuccess) return e;
+    size_t o = 0;
+    L.counts = o;   o += a256(nkeys * 4);
+    L.off = o;      o += a256(nkeys * 4);
+    L.keys = o;     o += a256(n * 4);
+    L.keys_out = o; o += a256(n * 4);
+    L.vals = o;     o += a256(n * 4);
+    L.vals_out = o; o += a256(n * 4);
+    L.delta = o;    o += a256(size_t(B * H * T) * 4);
+    L.scan_tmp = o; o += a256(L.scan_bytes);
+    L.sort_tmp = o; o += a256(L.sort_bytes);
+    L.total = o;
+    return hipSuccess;
+}
+
+template <typename DT>
+hipError_t launch_passes(const ReadoutBwdParams& p, hipStream_t s)
+{
+    const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
+    const dim3 g(static_cast<unsigned>(grid)), blk(64 * kWaves);
+    if (p.D == 32) {
+        readout_bwd_rows<DT, 32><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 32><<<g, blk, 0, s>>>(p);
+    } else if (p.D == 64) {
+        readout_bwd_rows<DT, 64><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 64><<<g, blk, 0, s>>>(p);
+    } else {
+        readout_bwd_rows<DT, 128><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 128><<<g, blk, 0, s>>>(p);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K, hipError_t* err)
+{
+    BwdLayout L{};
+    const hipError_t e = bwd_layout(B, H, T, K, L);
+    if (err) *err = e;
+    return e == hipSuccess ? L.total : 0;
+}
+
+hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s)
+{
+    BwdLayout L{};
+    hipError_t e = bwd_layout(p.B, p.H, p.T, p.K, L);
+    if (e != hipSuccess) return e;
+    if (ws_bytes < L.total) return hipErrorInvalidValue;
+    char* w = static_cast<char*>(ws);
+    uint32_t* counts = reinterpret_cast<uint32_t*>(w + L.counts);
+    uint32_t* off = reinterpret_cast<uint32_t*>(w + L.off);
+    uint32_t* keys = reinterpret_cast<uint32_t*>(w + L.keys);
+    uint32_t* keys_out = reinterpret_cast<uint32_t*>(w + L.keys_out);
+    uint32_t* vals = reinterpret_cast<uint32_t*>(w + L.vals);
+    uint32_t* vals_out = reinterpret_cast<uint32_t*>(w + L.vals_out);
+    const int64_t nkeys = p.B * p.T + 1;
+    const int64_t n = p.B * p.T * p.K;
+
+    // counts start at zero: a fill kernel rather than a memset node (graph-capture safe)
+    fill_u32<<<dim3(unsigned((nkeys + 255) / 256)), dim3(256), 0, s>>>(counts, nkeys, 0u);
+    bwd_transpose_keys<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(
+        p.idx, p.is[0], p.is[1], p.is[2], p.B, p.T, p.K, (p.flags & 1u) != 0, keys, vals, counts);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    size_t scan_bytes = L.scan_bytes;
+    e = rocprim::exclusive_scan(static_cast<void*>(w + L.scan_tmp), scan_bytes, static_cast<const uint32_t*>(counts),
+                                off, 0u, size_t(nkeys), rocprim::plus<uint32_t>(), s);
+    if (e != hipSuccess) return e;
+    size_t sort_bytes = L.sort_bytes;
+    e = rocprim::radix_sort_pairs(static_cast<void*>(w + L.sort_tmp), sort_bytes, static_cast<const uint32_t*>(keys),
+                                  keys_out, static_cast<const uint32_t*>(vals), vals_out, size_t(n), 0,
+                                  key_bits(p.B, p.T), s);
+    if (e != hipSuccess) return e;
+    p.delta = reinterpret_cast<float*>(w + L.delta);
+    p.off = off;
+    p.rows = vals_out;
+    if (dtype == 2) return launch_passes<bf16_t>(p, s);
+    if (dtype == 1) return launch_passes<_Float16>(p, s);
+    return launch_passes<float>(p, s);
+}
+
+}  // namespace wf

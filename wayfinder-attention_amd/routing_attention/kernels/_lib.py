@@ -46,6 +46,19 @@ class FusedArgs(ctypes.Structure):
     ]
 
 
+class ReadoutBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _p), ("k", _p), ("v", _p), ("dout", _p), ("indices", _p), ("lse2", _p),
+        ("dq", _p), ("dk", _p), ("dv", _p), ("workspace", _p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("q_strides", _i64 * 4), ("k_strides", _i64 * 4), ("v_strides", _i64 * 4),
+        ("dout_strides", _i64 * 4), ("dq_strides", _i64 * 4), ("dk_strides", _i64 * 4),
+        ("dv_strides", _i64 * 4), ("idx_strides", _i64 * 3),
+        ("B", _i64), ("H", _i64), ("T", _i64), ("D", _i64), ("K", _i64),
+        ("dtype", ctypes.c_int), ("scale", ctypes.c_float), ("flags", ctypes.c_uint),
+    ]
+
+
 SIGNATURES = {
     "wf_abi_version": (ctypes.c_int, []),
     "wf_last_error": (ctypes.c_char_p, []),
@@ -55,11 +68,16 @@ SIGNATURES = {
     "wf_sparse_readout_fwd": (ctypes.c_int, [_p, _p, _p, ctypes.c_int, _i64, _i64, _i64, _i64,
                                              _i64p, _i64p, _i64p, _p, _i64p, _i64,
                                              ctypes.c_float, ctypes.c_uint, _p, _i64p, _p]),
+    "wf_sparse_readout_fwd_lse": (ctypes.c_int, [_p, _p, _p, ctypes.c_int, _i64, _i64, _i64, _i64,
+                                                 _i64p, _i64p, _i64p, _p, _i64p, _i64,
+                                                 ctypes.c_float, ctypes.c_uint, _p, _i64p, _p, _p]),
+    "wf_sparse_readout_bwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
+    "wf_sparse_readout_bwd": (ctypes.c_int, [ctypes.POINTER(ReadoutBwdArgs), _p]),
     "wf_fused_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "wf_fused_topk_sparse_fwd": (ctypes.c_int, [ctypes.POINTER(FusedArgs), _p]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

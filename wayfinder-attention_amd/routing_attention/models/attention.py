@@ -8,8 +8,8 @@ With ``retrieval_config.use_fused_sparse`` each forward runs the fused HIP path
 (wf_fused_topk_sparse_fwd): retrieval and readout in one library call, no autograd, as the
 reference's @torch.no_grad fused_sparse_attention. Its output is written directly in
 (B, T, H, D) memory, so the head merge before out_proj is a view, not a copy. The other
-branch retrieves with the HIP causal top-K and reads out with the HIP readout when no
-gradient is needed.
+branch retrieves with the HIP causal top-K and reads out with the HIP readout, forward and
+backward; only dropout in training takes the reference's gather formulation.
 """
 
 from __future__ import annotations
@@ -25,6 +25,7 @@ from routing_attention.kernels.fused_sparse import (
     fused_sparse_attention_bthd,
     sparse_meat_attention,
 )
+from routing_attention.kernels.sparse_autograd import sparse_readout
 from routing_attention.models.learned_address import LearnedAddressModule
 from routing_attention.models.router import MultiScaleRouter, PerLayerRouter
 from routing_attention.retrieval.index import (
@@ -63,18 +64,21 @@ def _sparse_meat_forward(q, k, v, candidate_idx, scale: float, dropout: nn.Dropo
     """Attention of each query over its K candidates, (B, H, T, D) (reference
     attention.py:35-55).
 
-    * a gradient is needed, or dropout is active: the differentiable gather formulation
-      with dropout on the probabilities, as the reference's non-fused branch (torch ops
-      on the GPU).
-    * otherwise: the HIP readout ``sparse_meat_attention``.
+    * dropout active (training with p > 0): the gather formulation with dropout on the
+      probabilities, as the reference's non-fused branch (torch ops on the GPU);
+    * a gradient is needed: ``sparse_readout``, the HIP forward and backward (dq by a
+      row pass, dk/dv over the transposed index lists, deterministic);
+    * otherwise: the no-grad HIP readout ``sparse_meat_attention``.
     """
     del cfg
-    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
-    if needs_grad or (dropout.training and dropout.p > 0):
+    if dropout.training and dropout.p > 0:
         k_sel, v_sel = _gather_kv_heads(k, v, candidate_idx)
         scores = (q.unsqueeze(3) * k_sel).sum(-1) * scale
         attn = dropout(F.softmax(scores, dim=-1))
         return (attn.unsqueeze(-1) * v_sel).sum(dim=3)
+    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    if needs_grad:
+        return sparse_readout(q, k, v, candidate_idx, scale)
     return sparse_meat_attention(q, k, v, candidate_idx, scale)
 
 
