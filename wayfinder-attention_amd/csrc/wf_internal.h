@@ -140,7 +140,8 @@ struct ReadoutBwdParams {
     void* dv;
     const int32_t* idx;
     const float* lse2;       // (B, H, T) from the forward
-    float* delta;            // (B, H, T) workspace: sum_s p_s (dout . v_s), row pass -> key pass
+    float2* row_stats;       // (B, H, T) workspace, row pass -> key pass: (lse2, delta) with
+                             // delta = sum_s p_s (dout . v_s); one 8-byte load per list entry
     const uint32_t* off;     // (B*T + 1) start of each key's list in `rows`
     const uint32_t* rows;    // query rows t referencing each key, grouped by key, t ascending
     int64_t qs[4], ks[4], vs[4], gs[4], dqs[4], dks[4], dvs[4];  // element strides (B, H, T, D)

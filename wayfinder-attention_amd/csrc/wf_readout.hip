@@ -180,8 +180,10 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 // NB (even): wave steps per task. For 16-bit types the allocator is held to 128 registers
 // (4 waves per SIMD; two values spill to scratch): more gathers in flight per CU measured
 // 261 us against 275 us at 3 waves (T=16384, H=8, D=64, bf16).
-template <typename DT, int D, int NB>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(sizeof(DT) == 2 ? 4 : 1)))
+// LSE: also write the row's base-2 log-sum-exp (the training forward; it keeps 3 waves per
+// SIMD rather than spill the extra live values).
+template <typename DT, int D, int NB, bool LSE>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(sizeof(DT) == 2 && !LSE ? 4 : 1)))
 void sparse_readout_fast(ReadoutParams p)
 {
     static_assert(NB % 2 == 0, "steps are consumed in pairs");
@@ -222,6 +224,7 @@ void sparse_readout_fast(ReadoutParams p)
     const uint32_t qrow = uint32_t(p.qs[2]) * ES, orow = uint32_t(p.os[2]) * ES;
     const uint32_t loff = uint32_t(sub) * 8u * ES;
     const int32_t* ib = p.idx + b * p.is[0] + tw * p.is[1];
+    float* lrow = LSE ? p.lse2 + (b * p.H + h) * p.T + tw : nullptr;   // wave-uniform
     const int64_t irow = p.is[1];
 
     // stage I: offsets (+ query slice at a row's first task) of the task whose K/V load is next
@@ -295,7 +298,7 @@ void sparse_readout_fast(ReadoutParams p)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o8[e] *= inv;
                 store_row8<DT, true>(reinterpret_cast<DT*>(ob + uint32_t(rc) * orow + loff), 1, o8);
-                if (p.lse2 && sub == 0) p.lse2[(b * p.H + h) * p.T + t] = mm + log2f(lt);
+                if (LSE && sub == 0) lrow[rc] = mm + log2f(lt);
             }
         }
         advance(rc, qc);
@@ -339,7 +342,8 @@ hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
 #define WF_READOUT_FAST_NB 4
 #endif
     const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
-    sparse_readout_fast<DT, D, WF_READOUT_FAST_NB><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
+    if (p.lse2) sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, true><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
+    else sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, false><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
     return hipGetLastError();
 }
 

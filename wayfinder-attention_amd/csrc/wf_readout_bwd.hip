@@ -15,8 +15,9 @@
 //     offset; a stable rocPRIM radix sort of (b*T + j) keys with the query row t as value
 //     fills the lists, t ascending. Masked pad slots sort past the last list.
 //  2. row pass (the forward's mapping: one wave walks 4 query rows, D/8 lanes per
-//     neighbour): recomputes p from the forward's base-2 log-sum-exp and writes dq and
-//     delta (exact, from the row's own p and dp rather than the rounded output);
+//     neighbour): recomputes p from the forward's base-2 log-sum-exp and writes dq, and
+//     (lse2, delta) per row for the key pass -- delta exact, from the row's own p and dp
+//     rather than the rounded output;
 //  3. key pass (same mapping over key rows): each key row walks its list, gathering q_t and
 //     dout_t -- the forward's access pattern with the roles of query and key swapped -- and
 //     recomputes p and dp for every entry. Nothing of size (B, H, T, K) is stored.
@@ -38,23 +39,25 @@ __global__ void fill_u32(uint32_t* p, int64_t n, uint32_t v)
 // One thread per (b, t, s) slot: key b*T + j (j wrapped and clamped as in the forward),
 // value t. Masked pad slots (s > t on rows t < K-1 with WF_FLAG_MASK_PADS) carry no weight:
 // they get the key B*T, past every list, and are not counted.
+// B*T*K < 2^32 (checked by the entry point), so the slot arithmetic is 32-bit.
 __global__ void bwd_transpose_keys(const int32_t* idx, int64_t is0, int64_t is1, int64_t is2,
-                                   int64_t B, int64_t T, int64_t K, bool mask_pads,
+                                   uint32_t B, uint32_t T, uint32_t K, bool mask_pads,
                                    uint32_t* keys, uint32_t* vals, uint32_t* counts)
 {
-    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (e >= B * T * K) return;
-    const int64_t b = e / (T * K);
-    const int64_t r = e - b * T * K;
-    const int64_t t = r / K;
-    const int64_t s = r - t * K;
-    int64_t j = idx[b * is0 + t * is1 + s * is2];
-    if (j < 0) j += T;
-    j = j < 0 ? 0 : (j > T - 1 ? T - 1 : j);
-    const bool masked = mask_pads && t < K - 1 && s > t;
-    const uint32_t key = masked ? uint32_t(B * T) : uint32_t(b * T + j);
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t TK = T * K;
+    if (e >= B * TK) return;
+    const uint32_t b = e / TK;
+    const uint32_t r = e - b * TK;
+    const uint32_t t = r / K;
+    const uint32_t s = r - t * K;
+    int j = idx[int64_t(b) * is0 + int64_t(t) * is1 + int64_t(s) * is2];
+    j += (j >> 31) & int(T);
+    j = min(max(j, 0), int(T) - 1);
+    const bool masked = mask_pads && t + 1 < K && s > t;
+    const uint32_t key = masked ? B * T : b * T + uint32_t(j);
     keys[e] = key;
-    vals[e] = uint32_t(t);
+    vals[e] = t;
     if (!masked) atomicAdd(&counts[key], 1u);
 }
 
@@ -164,7 +167,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
         }
         if (grp == 0) {
             store_row8<DT, true>(reinterpret_cast<DT*>(db + uint32_t(r) * drow + loff), 1, o8);
-            if (sub == 0) p.delta[rbase + r] = delta;
+            if (sub == 0) p.row_stats[rbase + r] = make_float2(lt2, delta);
         }
     }
 }
@@ -195,8 +198,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams
     const uint32_t krow = uint32_t(p.ks[2]) * ES, vrow = uint32_t(p.vs[2]) * ES;
     const uint32_t dkrow = uint32_t(p.dks[2]) * ES, dvrow = uint32_t(p.dvs[2]) * ES;
     const uint32_t loff = uint32_t(sub) * 8u * ES;
-    const float* lse = p.lse2 + (b * p.H + h) * p.T;
-    const float* dl = p.delta + (b * p.H + h) * p.T;
+    const float2* rs = p.row_stats + (b * p.H + h) * p.T;
     const uint32_t* off = p.off + b * p.T + jw;
 
     for (int r = 0; r < w.n; ++r) {
@@ -210,21 +212,20 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams
             const uint32_t en[2] = {e + uint32_t(grp), e + uint32_t(NPS + grp)};
             int t[2];
             uint4 qlo[2], qhi[2], glo[2], ghi[2];
-            float lt2[2], dlt[2];
+            float2 st[2];   // (lse2, delta) of the entry's query row
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 t[u] = en[u] < e1 ? int(p.rows[en[u]]) : 0;
                 ld16<DT>(qb, uint32_t(t[u]) * qrow + loff, qlo[u], qhi[u]);
                 ld16<DT>(gb, uint32_t(t[u]) * grow + loff, glo[u], ghi[u]);
-                lt2[u] = lse[t[u]];
-                dlt[u] = dl[t[u]];
+                st[u] = rs[t[u]];
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float d = group_sum<LPN>(dot8<DT>(qlo[u], qhi[u], klo, khi));
                 const float dp = group_sum<LPN>(dot8<DT>(glo[u], ghi[u], vlo, vhi));
-                const float pu = en[u] < e1 ? exp2f(d * sl2 - lt2[u]) : 0.0f;
-                const float ds = pu * (dp - dlt[u]);
+                const float pu = en[u] < e1 ? exp2f(d * sl2 - st[u].x) : 0.0f;
+                const float ds = pu * (dp - st[u].y);
                 float qf[8], gf[8];
                 cvt8<DT>(qlo[u], qhi[u], qf);
                 cvt8<DT>(glo[u], ghi[u], gf);
@@ -259,7 +260,7 @@ int key_bits(int64_t B, int64_t T)
 }
 
 struct BwdLayout {
-    size_t counts, off, keys, keys_out, vals, vals_out, delta, scan_tmp, sort_tmp, total;
+    size_t counts, off, keys, keys_out, vals, vals_out, row_stats, scan_tmp, sort_tmp, total;
     size_t scan_bytes, sort_bytes;
 };
 
@@ -284,7 +285,7 @@ hipError_t bwd_layout(int64_t B, int64_t H, int64_t T, int64_t K, BwdLayout& L)
     L.keys_out = o; o += a256(n * 4);
     L.vals = o;     o += a256(n * 4);
     L.vals_out = o; o += a256(n * 4);
-    L.delta = o;    o += a256(size_t(B * H * T) * 4);
+    L.row_stats = o; o += a256(size_t(B * H * T) * 8);
     L.scan_tmp = o; o += a256(L.scan_bytes);
     L.sort_tmp = o; o += a256(L.sort_bytes);
     L.total = o;
@@ -338,7 +339,8 @@ hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, si
     // counts start at zero: a fill kernel rather than a memset node (graph-capture safe)
     fill_u32<<<dim3(unsigned((nkeys + 255) / 256)), dim3(256), 0, s>>>(counts, nkeys, 0u);
     bwd_transpose_keys<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(
-        p.idx, p.is[0], p.is[1], p.is[2], p.B, p.T, p.K, (p.flags & 1u) != 0, keys, vals, counts);
+        p.idx, p.is[0], p.is[1], p.is[2], uint32_t(p.B), uint32_t(p.T), uint32_t(p.K),
+        (p.flags & 1u) != 0, keys, vals, counts);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     size_t scan_bytes = L.scan_bytes;
@@ -350,7 +352,7 @@ hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, si
                                   keys_out, static_cast<const uint32_t*>(vals), vals_out, size_t(n), 0,
                                   key_bits(p.B, p.T), s);
     if (e != hipSuccess) return e;
-    p.delta = reinterpret_cast<float*>(w + L.delta);
+    p.row_stats = reinterpret_cast<float2*>(w + L.row_stats);
     p.off = off;
     p.rows = vals_out;
     if (dtype == 2) return launch_passes<bf16_t>(p, s);
