@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define WF_ABI_VERSION 2
+#define WF_ABI_VERSION 3
 
 typedef enum wf_status {
     WF_OK = 0,
@@ -168,6 +168,28 @@ size_t wf_sparse_readout_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, in
  * B*T*K < 2^32.
  */
 int wf_sparse_readout_bwd(const wf_readout_bwd_args* args, void* stream);
+
+/*
+ * Learned-address projection and L2 normalisation, both address streams in one pass.
+ * Replaces: LearnedAddressModule.forward_query_key
+ *           (routing_attention/models/learned_address.py:39-46):
+ *           q = normalize(x Wq^T + bq), k = normalize(x Wk^T + bk) (normalize = x / max(|x|, 1e-12)).
+ * x           : (B, T, d_model) of `dtype`, strides x_strides[3] (x_strides[2] == 1, 16-byte
+ *               aligned rows).
+ * wq, wk      : (R, d_model) nn.Linear weights of `dtype`, row stride w_stride (16-byte aligned
+ *               rows, unit column stride); bq, bk: (R) biases or NULL. wk == NULL: symmetric,
+ *               only out_q is written.
+ * out_q/out_k : (B, T, R) of `dtype`, strides oq_strides / ok_strides.
+ * normalize   : 0 = projections only.
+ * Rounding follows the PyTorch ops replaced: the projection is rounded to `dtype` (bias
+ * added in fp32), the norm of the rounded values accumulated in fp32 and rounded, the
+ * quotient computed in fp32 and rounded once. Limits: 1 <= R <= 32, d_model % 8 == 0.
+ */
+int wf_address_project_fwd(const void* x, int dtype, int64_t B, int64_t T, int64_t d_model,
+                           const int64_t* x_strides, const void* wq, const void* bq,
+                           const void* wk, const void* bk, int64_t w_stride, int64_t R,
+                           int normalize, void* out_q, const int64_t* oq_strides,
+                           void* out_k, const int64_t* ok_strides, void* stream);
 
 /* Arguments of the fused forward, one struct so the entry point stays stable. */
 typedef struct wf_fused_args {

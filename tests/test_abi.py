@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.wf_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.wf_abi_version() == _lib.ABI_VERSION == 3
 
 
 def _i64(*v):
@@ -193,3 +193,33 @@ def test_readout_fwd_lse_needs_lse(lib):
     rc = lib.wf_sparse_readout_fwd_lse(FAKE, FAKE, FAKE, 2, 1, 2, 64, 64, st, st, st, FAKE,
                                        _i64(64 * 8, 8, 1), 8, 0.125, 0, FAKE, st, None, None)
     assert rc == _lib.WF_ERR_INVALID_ARGUMENT and "lse2" in _lib.last_error()
+
+
+def _addr(lib, **kw):
+    a = dict(x=FAKE, dtype=2, B=1, T=16, D=64, xs=_i64(16 * 64, 64, 1), wq=FAKE, bq=None, wk=FAKE,
+             bk=None, ws=64, R=32, norm=1, oq=FAKE, oqs=_i64(16 * 32, 32, 1), ok=FAKE,
+             oks=_i64(16 * 32, 32, 1))
+    a.update(kw)
+    return lib.wf_address_project_fwd(a["x"], a["dtype"], a["B"], a["T"], a["D"], a["xs"], a["wq"],
+                                      a["bq"], a["wk"], a["bk"], a["ws"], a["R"], a["norm"], a["oq"],
+                                      a["oqs"], a["ok"], a["oks"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=5), _lib.WF_ERR_UNSUPPORTED, "dtype"),
+    (dict(R=33), _lib.WF_ERR_UNSUPPORTED, "R=33"),
+    (dict(D=60, ws=60), _lib.WF_ERR_UNSUPPORTED, "multiple of 8"),
+    (dict(R=0), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
+    (dict(x=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(ok=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(xs=_i64(16 * 64, 64, 2)), _lib.WF_ERR_UNSUPPORTED, "contiguous last dim"),
+    (dict(wq=FAKE + 4), _lib.WF_ERR_UNSUPPORTED, "16-byte"),
+    (dict(oks=None), _lib.WF_ERR_INVALID_ARGUMENT, "stride"),
+])
+def test_address_contract_errors(lib, kw, code, msg):
+    assert _addr(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_address_empty_is_noop(lib):
+    assert _addr(lib, B=0) == _lib.WF_OK

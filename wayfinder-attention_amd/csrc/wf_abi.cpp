@@ -304,6 +304,41 @@ int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
     return ok();
 }
 
+int wf_address_project_fwd(const void* x, int dtype, int64_t B, int64_t T, int64_t d_model,
+                           const int64_t* x_strides, const void* wq, const void* bq,
+                           const void* wk, const void* bk, int64_t w_stride, int64_t R,
+                           int normalize, void* out_q, const int64_t* oq_strides,
+                           void* out_k, const int64_t* ok_strides, void* stream)
+{
+    if (!valid_dtype(dtype)) return fail(WF_ERR_UNSUPPORTED, "address_project: unsupported dtype code %d", dtype);
+    if (B < 0 || T < 0 || d_model < 1 || R < 1)
+        return fail(WF_ERR_INVALID_ARGUMENT, "address_project: bad shape (B=%lld, T=%lld, d_model=%lld, R=%lld)",
+                    (long long)B, (long long)T, (long long)d_model, (long long)R);
+    if (R > 32) return fail(WF_ERR_UNSUPPORTED, "address_project: address dim R=%lld > 32", (long long)R);
+    if (d_model % 8 != 0) return fail(WF_ERR_UNSUPPORTED, "address_project: d_model=%lld not a multiple of 8", (long long)d_model);
+    if (!x_strides || !oq_strides || (wk && !ok_strides))
+        return fail(WF_ERR_INVALID_ARGUMENT, "address_project: stride arrays must not be NULL");
+    if (B * T == 0) return ok();
+    if (!x || !wq || !out_q || (wk && !out_k))
+        return fail(WF_ERR_INVALID_ARGUMENT, "address_project: NULL x/wq/out pointer");
+    const int64_t es = int64_t(elem_size(dtype));
+    auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (x_strides[2] != 1 || !a16(x) || (x_strides[0] * es) % 16 || (x_strides[1] * es) % 16)
+        return fail(WF_ERR_UNSUPPORTED, "address_project: x needs a contiguous last dim and 16-byte aligned rows");
+    if (!a16(wq) || (wk && !a16(wk)) || (w_stride * es) % 16 || w_stride < d_model)
+        return fail(WF_ERR_UNSUPPORTED, "address_project: weights need 16-byte aligned rows of at least d_model");
+    wf::AddressParams p{};
+    p.x = x; p.wq = wq; p.bq = bq; p.wk = wk; p.bk = bk; p.out_q = out_q; p.out_k = wk ? out_k : nullptr;
+    p.xs[0] = x_strides[0]; p.xs[1] = x_strides[1];
+    for (int i = 0; i < 3; ++i) { p.oqs[i] = oq_strides[i]; p.oks[i] = wk ? ok_strides[i] : 0; }
+    p.w_stride = w_stride;
+    p.B = B; p.T = T; p.d_model = d_model; p.R = R; p.n_tokens = B * T;
+    p.normalize = normalize ? 1 : 0;
+    const hipError_t e = wf::launch_address_project(dtype, p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("address_project: kernel launch", e);
+    return ok();
+}
+
 int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
 {
     if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "fused: NULL argument struct");

@@ -152,6 +152,22 @@ struct ReadoutBwdParams {
     int64_t seg_per_pair, rows_per_seg, vpairs, wg_per_vpair;   // as in ReadoutParams
 };
 
+// Learned-address projection + normalisation (wf_address.hip).
+struct AddressParams {
+    const void* x;           // (B, T, d_model), contiguous last dim
+    const void* wq;          // (R, d_model) rows at stride w_stride
+    const void* bq;          // (R) or null
+    const void* wk;          // null: symmetric (only q is written)
+    const void* bk;
+    void* out_q;             // (B, T, R)
+    void* out_k;             // null when symmetric
+    int64_t xs[2];           // element strides of x over (B, T)
+    int64_t oqs[3], oks[3];  // element strides of the outputs
+    int64_t w_stride;
+    int64_t B, T, d_model, R, n_tokens;
+    int normalize;
+};
+
 // Key-magnitude chunk size of the screening bound (keys per chunk).
 constexpr int kAbsmaxChunk = 256;
 // Query rows per readout workgroup (4 waves x 4 consecutive rows).
@@ -165,5 +181,6 @@ hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutPa
 // rocPRIM scan / sort scratch); 0 with *err set when rocPRIM cannot size it
 size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K, hipError_t* err);
 hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s);
+hipError_t launch_address_project(int dtype, const AddressParams& p, hipStream_t s);
 
 }  // namespace wf

@@ -73,11 +73,14 @@ SIGNATURES = {
                                                  ctypes.c_float, ctypes.c_uint, _p, _i64p, _p, _p]),
     "wf_sparse_readout_bwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "wf_sparse_readout_bwd": (ctypes.c_int, [ctypes.POINTER(ReadoutBwdArgs), _p]),
+    "wf_address_project_fwd": (ctypes.c_int, [_p, ctypes.c_int, _i64, _i64, _i64, _i64p, _p, _p,
+                                              _p, _p, _i64, _i64, ctypes.c_int, _p, _i64p, _p,
+                                              _i64p, _p]),
     "wf_fused_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "wf_fused_topk_sparse_fwd": (ctypes.c_int, [ctypes.POINTER(FusedArgs), _p]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

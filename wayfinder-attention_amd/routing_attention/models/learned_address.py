@@ -10,6 +10,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from routing_attention.kernels import address as address_kernel
+
 
 class LearnedAddressModule(nn.Module):
     """Maps hidden states to (query, key) addresses of dim ``address_dim`` used only for
@@ -32,7 +34,19 @@ class LearnedAddressModule(nn.Module):
 
     def forward_query_key(self, hidden: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """(B, T, d_model) -> two (B, T, address_dim) addresses, L2-normalised when
-        ``normalize`` (reference learned_address.py:39-46)."""
+        ``normalize`` (reference learned_address.py:39-46).
+
+        On a ROCm device with no gradient to carry, both projections and the normalisation
+        run as one HIP kernel (``wf_address_project_fwd``); otherwise the PyTorch ops."""
+        kp = self.k_addr_proj
+        needs_grad = torch.is_grad_enabled() and (
+            hidden.requires_grad or any(p.requires_grad for p in self.parameters()))
+        if not needs_grad and address_kernel.supported(hidden, self.q_addr_proj.weight,
+                                                       kp.weight if kp is not None else None):
+            return address_kernel.address_project(
+                hidden, self.q_addr_proj.weight, self.q_addr_proj.bias,
+                kp.weight if kp is not None else None, kp.bias if kp is not None else None,
+                normalize=self.normalize)
         q = self.q_addr_proj(hidden)
         k = self.k_addr_proj(hidden) if self.k_addr_proj is not None else q
         if self.normalize:
