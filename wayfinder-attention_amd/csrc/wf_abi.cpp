@@ -166,7 +166,9 @@ int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t 
     auto span_ok = [&](const int64_t* st) {
         return st[2] >= 0 && (T - 1) * st[2] * es + D * es < (int64_t(1) << 32);
     };
-    const bool fast = vec && is[2] == 1 && span_ok(qs) && span_ok(ks) && span_ok(vs) && span_ok(os);
+    // the fast kernel forms row offsets with 24-bit multiplies
+    const bool mul24 = T <= (int64_t(1) << 24) && ks[2] * es < (int64_t(1) << 24) && vs[2] * es < (int64_t(1) << 24);
+    const bool fast = vec && is[2] == 1 && span_ok(qs) && span_ok(ks) && span_ok(vs) && span_ok(os) && mul24;
     const hipError_t e = wf::launch_sparse_readout(dtype, vec, fast, p, stream);
     if (e != hipSuccess) return hip_fail("sparse_readout: kernel launch", e);
     return WF_OK;
@@ -216,7 +218,7 @@ int wf_sparse_readout_fwd(const void* q, const void* k, const void* v, int dtype
                            idx_strides, K, out, out_strides);
     if (rc != WF_OK) return rc;
     rc = run_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
-                     idx_strides, K, scale, flags, out, out_strides, nullptr,
+                     idx_strides, K, scale, flags & WF_FLAG_MASK_PADS, out, out_strides, nullptr,
                      static_cast<hipStream_t>(stream));
     return rc == WF_OK ? ok() : rc;
 }
@@ -233,7 +235,7 @@ int wf_sparse_readout_fwd_lse(const void* q, const void* k, const void* v, int d
     if (rc != WF_OK) return rc;
     if (!lse2 && B * H * T > 0) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_fwd_lse: NULL lse2");
     rc = run_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
-                     idx_strides, K, scale, flags, out, out_strides, lse2,
+                     idx_strides, K, scale, flags & WF_FLAG_MASK_PADS, out, out_strides, lse2,
                      static_cast<hipStream_t>(stream));
     return rc == WF_OK ? ok() : rc;
 }
@@ -291,7 +293,7 @@ int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
     }
     for (int i = 0; i < 3; ++i) p.is[i] = a->idx_strides[i];
     p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
-    p.scale = a->scale; p.flags = a->flags;
+    p.scale = a->scale; p.flags = a->flags & WF_FLAG_MASK_PADS;
     const int64_t nbh = B * H;
     p.seg_per_pair = 8 / gcd64(nbh, 8);
     p.rows_per_seg = cdiv(T, p.seg_per_pair);
@@ -358,9 +360,11 @@ int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
                   a->ks_strides, a->top_k, a->out_idx, a->out_scores, a->workspace,
                   a->workspace_bytes, s);
     if (rc != WF_OK) return rc;
+    // the indices were just written by the retrieval: all in [0, T)
     rc = run_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
-                     a->k_strides, a->v_strides, a->out_idx, is, k_eff, a->scale, a->flags,
-                     a->out, a->out_strides, nullptr, s);
+                     a->k_strides, a->v_strides, a->out_idx, is, k_eff, a->scale,
+                     (a->flags & WF_FLAG_MASK_PADS) | wf::kFlagTrustedIndices, a->out, a->out_strides,
+                     nullptr, s);
     return rc == WF_OK ? ok() : rc;
 }
 

@@ -168,6 +168,10 @@ struct AddressParams {
     int normalize;
 };
 
+// ReadoutParams.flags bit set by the fused entry point: the indices were written by this
+// library's retrieval, so every entry lies in [0, T) and needs no wrap or clamp.
+constexpr unsigned kFlagTrustedIndices = 0x80000000u;
+
 // Key-magnitude chunk size of the screening bound (keys per chunk).
 constexpr int kAbsmaxChunk = 256;
 // Query rows per readout workgroup (4 waves x 4 consecutive rows).

@@ -181,8 +181,11 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 // (4 waves per SIMD; two values spill to scratch): more gathers in flight per CU measured
 // 261 us against 275 us at 3 waves (T=16384, H=8, D=64, bf16).
 // LSE: also write the row's base-2 log-sum-exp (the training forward; it keeps 3 waves per
-// SIMD rather than spill the extra live values).
-template <typename DT, int D, int NB, bool LSE>
+// SIMD rather than spill the extra live values). TRUST: the indices are known to lie in
+// [0, T) (they come from this library's retrieval), so the wrap/clamp is skipped.
+// Byte offsets of gathered rows use 24-bit multiplies (T and the row strides below 2^24,
+// checked by the host).
+template <typename DT, int D, int NB, bool LSE, bool TRUST>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(sizeof(DT) == 2 && !LSE ? 4 : 1)))
 void sparse_readout_fast(ReadoutParams p)
 {
@@ -237,10 +240,12 @@ void sparse_readout_fast(ReadoutParams p)
         for (int u = 0; u < NB; ++u) {
             const int slot = min(qi * CH + u * NPS + grp, K - 1);
             int j = *reinterpret_cast<const int*>(ip + uint32_t(slot) * 4u);
-            j += (j >> 31) & T;
-            j = min(max(j, 0), T - 1);
-            ko[u] = uint32_t(j) * krow + loff;
-            vo[u] = uint32_t(j) * vrow + loff;
+            if constexpr (!TRUST) {
+                j += (j >> 31) & T;
+                j = min(max(j, 0), T - 1);
+            }
+            ko[u] = __umul24(uint32_t(j), krow) + loff;
+            vo[u] = __umul24(uint32_t(j), vrow) + loff;
         }
         if (qi == 0) ld16<DT>(qb, uint32_t(ri) * qrow + loff, qIlo, qIhi);
     };
@@ -267,28 +272,40 @@ void sparse_readout_fast(ReadoutParams p)
         const int lim = (mask_flag && t < K - 1) ? t + 1 : K;   // slots >= lim carry no weight
         float sc[NB];
         float bm = -__builtin_inff();
+        if (lim >= (qc + 1) * CH) {   // wave-uniform: every slot of this task counts
 #pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
-            sc[u] = slot0 + u * NPS < lim ? d * sl2 : -__builtin_inff();
-            bm = fmaxf(bm, sc[u]);
+            for (int u = 0; u < NB; ++u) {
+                sc[u] = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u])) * sl2;
+                bm = fmaxf(bm, sc[u]);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
+                sc[u] = slot0 + u * NPS < lim ? d * sl2 : -__builtin_inff();
+                bm = fmaxf(bm, sc[u]);
+            }
         }
+        // v_exp_f32 directly (2^-inf = 0); ms keeps the arguments off -inf - -inf while
+        // every slot seen so far is masked. Results below 2^-126 flush to zero, far below
+        // the weights that matter after the max is subtracted.
         const float mn = fmaxf(m, bm);
-        const float alpha = m == -__builtin_inff() ? 0.0f : exp2f(m - mn);
+        const float ms = mn == -__builtin_inff() ? 0.0f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m - ms);
         l *= alpha;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
         for (int u = 0; u < NB; u += 2) {
-            const float pa = sc[u] == -__builtin_inff() ? 0.0f : exp2f(sc[u] - mn);
-            const float pc = sc[u + 1] == -__builtin_inff() ? 0.0f : exp2f(sc[u + 1] - mn);
+            const float pa = __builtin_amdgcn_exp2f(sc[u] - ms);
+            const float pc = __builtin_amdgcn_exp2f(sc[u + 1] - ms);
             l += pa + pc;
             pv2<DT>(acc, pa, pc, vlo[u], vhi[u], vlo[u + 1], vhi[u + 1]);
         }
         m = mn;
         if (qc == nb - 1) {
             const float mm = group_allreduce<LPN, true>(m);
-            const float f = m == -__builtin_inff() ? 0.0f : exp2f(m - mm);
+            const float f = __builtin_amdgcn_exp2f(m - (mm == -__builtin_inff() ? 0.0f : mm));
             const float lt = group_allreduce<LPN, false>(l * f);
             float o8[8];
 #pragma unroll
@@ -342,8 +359,10 @@ hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
 #define WF_READOUT_FAST_NB 4
 #endif
     const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
-    if (p.lse2) sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, true><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
-    else sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, false><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
+    const dim3 g(static_cast<unsigned>(grid)), blk(64 * kWaves);
+    if (p.lse2) sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, true, false><<<g, blk, 0, s>>>(p);
+    else if (p.flags & kFlagTrustedIndices) sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, false, true><<<g, blk, 0, s>>>(p);
+    else sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, false, false><<<g, blk, 0, s>>>(p);
     return hipGetLastError();
 }
 

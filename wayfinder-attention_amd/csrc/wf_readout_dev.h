@@ -71,18 +71,24 @@ __device__ __forceinline__ void store_row8(DT* p, int64_t sd, const float* f)
 }
 
 // ---------------------------------------------------------------- reductions
-// Sum over the LPN lanes that share one neighbour (LPN in {4, 8, 16}), with DPP moves:
-// quad_perm xor 1 and xor 2 sum each quad; row_half_mirror then adds the other quad of the
-// 8-lane group and row_mirror the other half of the 16-lane row.
+// Sum over the LPN lanes that share one neighbour (LPN in {4, 8, 16}), with DPP: quad_perm
+// xor 1 and xor 2 sum each quad; row_half_mirror then adds the other quad of the 8-lane
+// group and row_mirror the other half of the 16-lane row. Every pattern reads a valid lane,
+// so bound_ctrl changes nothing; written as update_dpp(0, x, ...) the compiler folds each
+// move into the add (one v_add_f32_dpp per level).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+
 template <int LPN>
 __device__ __forceinline__ float group_sum(float x)
 {
-    x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xf, 0xf, false));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xf, 0xf, false));
-    if constexpr (LPN >= 8)
-        x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xf, 0xf, false));
-    if constexpr (LPN >= 16)
-        x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xf, 0xf, false));
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    if constexpr (LPN >= 8) x += dpp<0x141>(x);
+    if constexpr (LPN >= 16) x += dpp<0x140>(x);
     return x;
 }
 
@@ -133,7 +139,7 @@ __device__ __forceinline__ float dot8(const uint4& qlo, const uint4& qhi, const 
 template <int N>   // rotate right by N lanes within each 16-lane row
 __device__ __forceinline__ float dpp_ror(float x)
 {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 + N, 0xf, 0xf, false));
+    return dpp<0x120 + N>(x);
 }
 
 // op over the lane groups of the wave (groups = lanes with equal bits below LPN): DPP
