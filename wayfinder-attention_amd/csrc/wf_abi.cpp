@@ -106,17 +106,11 @@ int hip_fail(const char* what, hipError_t e)
     return fail(WF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T, int64_t R,
-             const int64_t* qs, const int64_t* ks, int64_t top_k, int32_t* out_idx,
-             float* out_scores, void* ws, size_t ws_bytes, hipStream_t stream)
+bool topk_prepare(const void* query, const void* key, int dtype, int64_t B, int64_t T, int64_t R,
+                  const int64_t* qs, const int64_t* ks, int64_t k_eff, int32_t* out_idx,
+                  float* out_scores, void* ws, wf::TopkParams& p)
 {
-    const int64_t k_eff = std::min(top_k, T);
-    if (B == 0 || k_eff == 0) return WF_OK;
-    const size_t need = wf_causal_topk_workspace_bytes(B, T, R, top_k);
-    if (!ws || ws_bytes < need)
-        return fail(WF_ERR_WORKSPACE, "causal_topk: workspace of %zu bytes required, got %zu", need, ws ? ws_bytes : size_t(0));
-    if (reinterpret_cast<uintptr_t>(ws) % 4 != 0) return fail(WF_ERR_INVALID_ARGUMENT, "causal_topk: workspace not 4-byte aligned");
-    wf::TopkParams p{};
+    p = wf::TopkParams{};
     p.query = query; p.key = key;
     p.qsb = qs[0]; p.qst = qs[1]; p.qsr = qs[2];
     p.ksb = ks[0]; p.kst = ks[1]; p.ksr = ks[2];
@@ -125,11 +119,34 @@ int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T
     p.chunk_absmax = static_cast<float*>(ws);
     p.n_chunks = cdiv(T, wf::kAbsmaxChunk);
     p.n_row_blocks = cdiv(T, 16);
+    p.rb_begin = 0;
+    p.rb_end = p.n_row_blocks;
     // vector loads; key rows are addressed with 32-bit byte offsets from the batch base and
     // every 32-dim chunk the kernel reads lies inside the row (R = 32, 64 or 128)
-    const bool vec = (R == 32 || R == 64 || R == 128) &&
-                     vec_ok(query, dtype, qs, 3, R) && vec_ok(key, dtype, ks, 3, R) &&
-                     ks[1] >= 0 && (T - 1) * ks[1] * int64_t(elem_size(dtype)) + R * int64_t(elem_size(dtype)) < (int64_t(1) << 32);
+    return (R == 32 || R == 64 || R == 128) &&
+           vec_ok(query, dtype, qs, 3, R) && vec_ok(key, dtype, ks, 3, R) &&
+           ks[1] >= 0 && (T - 1) * ks[1] * int64_t(elem_size(dtype)) + R * int64_t(elem_size(dtype)) < (int64_t(1) << 32);
+}
+
+int check_topk_ws(int64_t B, int64_t T, int64_t R, int64_t top_k, void* ws, size_t ws_bytes)
+{
+    const size_t need = wf_causal_topk_workspace_bytes(B, T, R, top_k);
+    if (!ws || ws_bytes < need)
+        return fail(WF_ERR_WORKSPACE, "causal_topk: workspace of %zu bytes required, got %zu", need, ws ? ws_bytes : size_t(0));
+    if (reinterpret_cast<uintptr_t>(ws) % 4 != 0) return fail(WF_ERR_INVALID_ARGUMENT, "causal_topk: workspace not 4-byte aligned");
+    return WF_OK;
+}
+
+int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T, int64_t R,
+             const int64_t* qs, const int64_t* ks, int64_t top_k, int32_t* out_idx,
+             float* out_scores, void* ws, size_t ws_bytes, hipStream_t stream)
+{
+    const int64_t k_eff = std::min(top_k, T);
+    if (B == 0 || k_eff == 0) return WF_OK;
+    const int rc = check_topk_ws(B, T, R, top_k, ws, ws_bytes);
+    if (rc != WF_OK) return rc;
+    wf::TopkParams p;
+    const bool vec = topk_prepare(query, key, dtype, B, T, R, qs, ks, k_eff, out_idx, out_scores, ws, p);
     hipError_t e = wf::launch_key_absmax(dtype, vec, p, stream);
     if (e != hipSuccess) return hip_fail("causal_topk: key magnitude kernel launch", e);
     e = wf::launch_causal_topk(dtype, vec, p, stream);
@@ -137,29 +154,36 @@ int run_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T
     return WF_OK;
 }
 
-int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
-                int64_t T, int64_t D, const int64_t* qs, const int64_t* ks, const int64_t* vs,
-                const int32_t* idx, const int64_t* is, int64_t K, float scale, unsigned flags,
-                void* out, const int64_t* os, float* lse2, hipStream_t stream)
+// Point a readout launch at query rows [r0, r1): split each (b, h) pair into row segments
+// so that the number of virtual pairs is a multiple of the 8 XCDs. False if too large.
+bool readout_rows(wf::ReadoutParams& p, int64_t r0, int64_t r1)
 {
-    if (B * H * T == 0) return WF_OK;
-    wf::ReadoutParams p{};
+    const int64_t nbh = p.B * p.H;
+    p.row_begin = r0;
+    p.row_end = r1;
+    p.seg_per_pair = 8 / gcd64(nbh, 8);
+    p.rows_per_seg = cdiv(r1 - r0, p.seg_per_pair);
+    p.vpairs = nbh * p.seg_per_pair;
+    p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
+    return p.vpairs * p.wg_per_vpair < (int64_t(1) << 31);
+}
+
+// Readout parameters for query rows [row_begin, row_end); returns false if the problem is
+// too large for one launch. *fast selects the aligned kernel.
+bool readout_prepare(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                     int64_t T, int64_t D, const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                     const int32_t* idx, const int64_t* is, int64_t K, float scale, unsigned flags,
+                     void* out, const int64_t* os, float* lse2, wf::ReadoutParams& p, bool* vec,
+                     bool* fast)
+{
+    p = wf::ReadoutParams{};
     p.q = q; p.k = k; p.v = v; p.out = out; p.idx = idx; p.lse2 = lse2;
     for (int i = 0; i < 4; ++i) { p.qs[i] = qs[i]; p.ks[i] = ks[i]; p.vs[i] = vs[i]; p.os[i] = os[i]; }
     for (int i = 0; i < 3; ++i) p.is[i] = is[i];
     p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
     p.scale = scale; p.flags = flags;
-    // split each (b, h) pair into row segments so that the number of virtual pairs is a
-    // multiple of the 8 XCDs
-    const int64_t nbh = B * H;
-    p.seg_per_pair = 8 / gcd64(nbh, 8);
-    p.rows_per_seg = cdiv(T, p.seg_per_pair);
-    p.vpairs = nbh * p.seg_per_pair;
-    p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
-    const int64_t grid = p.vpairs * p.wg_per_vpair;
-    if (grid >= (int64_t(1) << 31)) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: problem too large for one launch");
-    const bool vec = vec_ok(q, dtype, qs, 4, D) && vec_ok(k, dtype, ks, 4, D) &&
-                     vec_ok(v, dtype, vs, 4, D) && vec_ok(out, dtype, os, 4, D);
+    *vec = vec_ok(q, dtype, qs, 4, D) && vec_ok(k, dtype, ks, 4, D) && vec_ok(v, dtype, vs, 4, D) &&
+           vec_ok(out, dtype, os, 4, D);
     // fast path: 32-bit byte offsets cover each (b, h) span of q/k/v/out, contiguous index
     // rows, non-negative row strides
     const int64_t es = int64_t(elem_size(dtype));
@@ -168,7 +192,21 @@ int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t 
     };
     // the fast kernel forms row offsets with 24-bit multiplies
     const bool mul24 = T <= (int64_t(1) << 24) && ks[2] * es < (int64_t(1) << 24) && vs[2] * es < (int64_t(1) << 24);
-    const bool fast = vec && is[2] == 1 && span_ok(qs) && span_ok(ks) && span_ok(vs) && span_ok(os) && mul24;
+    *fast = *vec && is[2] == 1 && span_ok(qs) && span_ok(ks) && span_ok(vs) && span_ok(os) && mul24;
+    return readout_rows(p, 0, T);
+}
+
+int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                int64_t T, int64_t D, const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                const int32_t* idx, const int64_t* is, int64_t K, float scale, unsigned flags,
+                void* out, const int64_t* os, float* lse2, hipStream_t stream)
+{
+    if (B * H * T == 0) return WF_OK;
+    wf::ReadoutParams p;
+    bool vec, fast;
+    if (!readout_prepare(q, k, v, dtype, B, H, T, D, qs, ks, vs, idx, is, K, scale, flags, out, os,
+                         lse2, p, &vec, &fast))
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout: problem too large for one launch");
     const hipError_t e = wf::launch_sparse_readout(dtype, vec, fast, p, stream);
     if (e != hipSuccess) return hip_fail("sparse_readout: kernel launch", e);
     return WF_OK;
@@ -295,6 +333,8 @@ int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
     p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
     p.scale = a->scale; p.flags = a->flags & WF_FLAG_MASK_PADS;
     const int64_t nbh = B * H;
+    p.row_begin = 0;
+    p.row_end = T;
     p.seg_per_pair = 8 / gcd64(nbh, 8);
     p.rows_per_seg = cdiv(T, p.seg_per_pair);
     p.vpairs = nbh * p.seg_per_pair;
@@ -347,25 +387,39 @@ int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
     int rc = check_topk(a->q_search, a->k_search, a->search_dtype, a->B, a->T, a->R,
                         a->qs_strides, a->ks_strides, a->top_k, a->out_idx);
     if (rc != WF_OK) return rc;
-    const int64_t k_eff = std::min(a->top_k, a->T);
-    if (k_eff < 1 && a->B * a->T > 0)
+    const int64_t B = a->B, T = a->T;
+    const int64_t k_eff = std::min(a->top_k, T);
+    if (k_eff < 1 && B * T > 0)
         return fail(WF_ERR_INVALID_ARGUMENT, "fused: top_k must be >= 1 (empty selections have no readout)");
-    const int64_t is[3] = {a->T * k_eff, k_eff, 1};
-    rc = check_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
+    const int64_t is[3] = {T * k_eff, k_eff, 1};
+    rc = check_readout(a->q, a->k, a->v, a->dtype, B, a->H, T, a->D, a->q_strides,
                        a->k_strides, a->v_strides, a->out_idx, is, k_eff > 0 ? k_eff : 1, a->out,
                        a->out_strides);
     if (rc != WF_OK) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    rc = run_topk(a->q_search, a->k_search, a->search_dtype, a->B, a->T, a->R, a->qs_strides,
-                  a->ks_strides, a->top_k, a->out_idx, a->out_scores, a->workspace,
-                  a->workspace_bytes, s);
+    if (B * T == 0 || a->H == 0) return ok();
+    rc = check_topk_ws(B, T, a->R, a->top_k, a->workspace, a->workspace_bytes);
     if (rc != WF_OK) return rc;
-    // the indices were just written by the retrieval: all in [0, T)
-    rc = run_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
-                     a->k_strides, a->v_strides, a->out_idx, is, k_eff, a->scale,
-                     (a->flags & WF_FLAG_MASK_PADS) | wf::kFlagTrustedIndices, a->out, a->out_strides,
-                     nullptr, s);
-    return rc == WF_OK ? ok() : rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    wf::TopkParams tp;
+    const bool tvec = topk_prepare(a->q_search, a->k_search, a->search_dtype, B, T, a->R, a->qs_strides,
+                                   a->ks_strides, k_eff, a->out_idx, a->out_scores, a->workspace, tp);
+    // the readout's indices are written by the retrieval just before: all in [0, T)
+    wf::ReadoutParams rp;
+    bool rvec, rfast;
+    if (!readout_prepare(a->q, a->k, a->v, a->dtype, B, a->H, T, a->D, a->q_strides, a->k_strides,
+                         a->v_strides, a->out_idx, is, k_eff, a->scale,
+                         (a->flags & WF_FLAG_MASK_PADS) | wf::kFlagTrustedIndices, a->out,
+                         a->out_strides, nullptr, rp, &rvec, &rfast))
+        return fail(WF_ERR_UNSUPPORTED, "fused: problem too large for one launch");
+
+    hipError_t e = wf::launch_key_absmax(a->search_dtype, tvec, tp, s);
+    if (e != hipSuccess) return hip_fail("fused: key magnitude kernel launch", e);
+    e = wf::launch_causal_topk(a->search_dtype, tvec, tp, s);
+    if (e != hipSuccess) return hip_fail("fused: retrieval kernel launch", e);
+    e = wf::launch_sparse_readout(a->dtype, rvec, rfast, rp, s);
+    if (e != hipSuccess) return hip_fail("fused: readout kernel launch", e);
+    return ok();
 }
 
 }  // extern "C"

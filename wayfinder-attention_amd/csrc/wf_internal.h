@@ -107,6 +107,7 @@ struct TopkParams {
     float* chunk_absmax;     // (B, n_chunks) workspace
     int64_t n_chunks;
     int64_t n_row_blocks;    // ceil(T / 16)
+    int64_t rb_begin, rb_end;  // row blocks [rb_begin, rb_end) of this launch
 };
 
 struct ReadoutParams {
@@ -122,6 +123,7 @@ struct ReadoutParams {
     unsigned flags;
     float* lse2;            // optional (B, H, T) contiguous: log2 of the softmax denominator
                             // in the kernels' base-2 domain (see wf_sparse_readout_fwd_lse)
+    int64_t row_begin, row_end;  // query rows [row_begin, row_end) of this launch
     int64_t seg_per_pair;   // row segments per (b,h) pair (XCD balance)
     int64_t rows_per_seg;
     int64_t vpairs;         // B*H*seg_per_pair virtual pairs
@@ -149,7 +151,8 @@ struct ReadoutBwdParams {
     int64_t B, H, T, D, K;
     float scale;
     unsigned flags;
-    int64_t seg_per_pair, rows_per_seg, vpairs, wg_per_vpair;   // as in ReadoutParams
+    int64_t row_begin, row_end;                                 // as in ReadoutParams
+    int64_t seg_per_pair, rows_per_seg, vpairs, wg_per_vpair;
 };
 
 // Learned-address projection + normalisation (wf_address.hip).

@@ -50,8 +50,8 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
     const int64_t pair = vp / p.seg_per_pair;
     const int64_t seg = vp % p.seg_per_pair;
     const int64_t b = pair / p.H, h = pair % p.H;
-    const int64_t t0 = seg * p.rows_per_seg;
-    const int64_t t1 = min(p.T, t0 + p.rows_per_seg);
+    const int64_t t0 = p.row_begin + seg * p.rows_per_seg;
+    const int64_t t1 = min(p.row_end, t0 + p.rows_per_seg);
     const int64_t tw = t0 + (chunk * kWaves + wave) * kRowsPerWave;   // first row of this wave
     if (tw >= t1) return;
     const int nrows = int(min(int64_t(kRowsPerWave), t1 - tw));
@@ -207,8 +207,8 @@ void sparse_readout_fast(ReadoutParams p)
     const int64_t pair = vp / p.seg_per_pair;
     const int64_t seg = vp % p.seg_per_pair;
     const int64_t b = pair / p.H, h = pair % p.H;
-    const int64_t t0 = seg * p.rows_per_seg;
-    const int64_t t1 = min(p.T, t0 + p.rows_per_seg);
+    const int64_t t0 = p.row_begin + seg * p.rows_per_seg;
+    const int64_t t1 = min(p.row_end, t0 + p.rows_per_seg);
     const int64_t tw = t0 + (chunk * kWaves + wave) * kRowsPerWave;
     if (tw >= t1) return;
     const int nrows = int(min(int64_t(kRowsPerWave), t1 - tw));

@@ -77,8 +77,8 @@ __device__ __forceinline__ Pair map_rows(const ReadoutBwdParams& p, int wave)
     const int64_t seg = vp % p.seg_per_pair;
     r.b = pair / p.H;
     r.h = pair % p.H;
-    const int64_t t0 = seg * p.rows_per_seg;
-    const int64_t t1 = min(p.T, t0 + p.rows_per_seg);
+    const int64_t t0 = p.row_begin + seg * p.rows_per_seg;
+    const int64_t t1 = min(p.row_end, t0 + p.rows_per_seg);
     r.r0 = t0 + (chunk * kWaves + wave) * kRowsPerWave;
     if (r.r0 < t1) r.n = int(min(int64_t(kRowsPerWave), t1 - r.r0));
     return r;

@@ -629,7 +629,7 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
 
     const int64_t T = p.T;
     const int64_t b = blockIdx.x % p.B;
-    const int64_t rb = p.n_row_blocks - 1 - blockIdx.x / p.B;   // longest prefixes first
+    const int64_t rb = p.rb_end - 1 - blockIdx.x / p.B;   // longest prefixes first
     const int64_t r0 = rb * kRows;
     const int64_t row = r0 + n;
     const bool row_ok = row < T;
@@ -871,7 +871,7 @@ __global__ __launch_bounds__(64 * kWaves) void causal_topk_wide_kernel(TopkParam
 template <typename DT, bool VEC, int RC, int KP2>
 void launch_topk_kp(const TopkParams& p, hipStream_t s)
 {
-    const dim3 grid(unsigned(p.B * p.n_row_blocks)), block(64 * kWaves);
+    const dim3 grid(unsigned(p.B * (p.rb_end - p.rb_begin))), block(64 * kWaves);
     if constexpr (RC <= 2) causal_topk_kernel<DT, VEC, RC, KP2><<<grid, block, 0, s>>>(p);
     else causal_topk_wide_kernel<DT, VEC, RC, KP2><<<grid, block, 0, s>>>(p);
 }
