@@ -11,9 +11,10 @@
 //   dv_j = sum_{(t,s): j_s = j} p_s dout_t
 //
 // computed without floating-point atomics, so the gradients are deterministic:
-//  1. index transpose: a counting pass and an exclusive scan give each key j its list
-//     offset; a stable rocPRIM radix sort of (b*T + j) keys with the query row t as value
-//     fills the lists, t ascending. Masked pad slots sort past the last list.
+//  1. index transpose: a stable rocPRIM radix sort of (b*T + j) keys with the query row t
+//     as value groups the rows that selected each key, t ascending; a binary search per key
+//     over the sorted keys gives each list's offset. Masked pad slots sort past the last
+//     list.
 //  2. row pass (the forward's mapping: one wave walks 4 query rows, D/8 lanes per
 //     neighbour): recomputes p from the forward's base-2 log-sum-exp and writes dq, and
 //     (lse2, delta) per row for the key pass -- delta exact, from the row's own p and dp
@@ -23,26 +24,19 @@
 //     recomputes p and dp for every entry. Nothing of size (B, H, T, K) is stored.
 // All accumulation is fp32; each gradient element is rounded once to the input dtype.
 #include <rocprim/device/device_radix_sort.hpp>
-#include <rocprim/device/device_scan.hpp>
 
 #include "wf_readout_dev.h"
 
 namespace wf {
 namespace {
 
-__global__ void fill_u32(uint32_t* p, int64_t n, uint32_t v)
-{
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = v;
-}
-
 // One thread per (b, t, s) slot: key b*T + j (j wrapped and clamped as in the forward),
 // value t. Masked pad slots (s > t on rows t < K-1 with WF_FLAG_MASK_PADS) carry no weight:
-// they get the key B*T, past every list, and are not counted.
-// B*T*K < 2^32 (checked by the entry point), so the slot arithmetic is 32-bit.
+// they get the key B*T, which sorts past every list. B*T*K < 2^32 (checked by the entry
+// point), so the slot arithmetic is 32-bit.
 __global__ void bwd_transpose_keys(const int32_t* idx, int64_t is0, int64_t is1, int64_t is2,
                                    uint32_t B, uint32_t T, uint32_t K, bool mask_pads,
-                                   uint32_t* keys, uint32_t* vals, uint32_t* counts)
+                                   uint32_t* keys, uint32_t* vals)
 {
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
     const uint32_t TK = T * K;
@@ -55,10 +49,23 @@ __global__ void bwd_transpose_keys(const int32_t* idx, int64_t is0, int64_t is1,
     j += (j >> 31) & int(T);
     j = min(max(j, 0), int(T) - 1);
     const bool masked = mask_pads && t + 1 < K && s > t;
-    const uint32_t key = masked ? B * T : b * T + uint32_t(j);
-    keys[e] = key;
+    keys[e] = masked ? B * T : b * T + uint32_t(j);
     vals[e] = t;
-    if (!masked) atomicAdd(&counts[key], 1u);
+}
+
+// off[k] = first position of the sorted keys holding a key >= k, for k = 0 .. B*T: the start
+// of key k's list (off[B*T] = the number of unmasked slots). One binary search per key.
+__global__ void bwd_list_offsets(const uint32_t* sorted, uint32_t n, uint32_t nkeys, uint32_t* off)
+{
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= nkeys) return;
+    uint32_t lo = 0, hi = n;   // invariant: sorted[lo-1] < k <= sorted[hi]
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (sorted[mid] < k) lo = mid + 1;
+        else hi = mid;
+    }
+    off[k] = lo;
 }
 
 struct Pair { int64_t b, h, r0; int n; };
@@ -141,21 +148,19 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
                 ld16<DT>(kb, uint32_t(j) * krow + loff, klo[u], khi[u]);
                 ld16<DT>(vb, uint32_t(j) * vrow + loff, vlo[u], vhi[u]);
             }
+            float pu[2], pd[2];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
                 const float dp = group_sum<LPN>(dot8<DT>(glo, ghi, vlo[u], vhi[u]));
-                const float pu = sl[u] < lim ? exp2f(d * sl2 - lt2) : 0.0f;
-                const float pd = pu * dp;
-                dsum += pd;
-                float kf[8];
-                cvt8<DT>(klo[u], khi[u], kf);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    A[e] = fmaf(pd, kf[e], A[e]);
-                    Bk[e] = fmaf(pu, kf[e], Bk[e]);
-                }
+                // v_exp_f32 directly: 2^(s - lse) <= 1; masked slots get no weight
+                pu[u] = sl[u] < lim ? __builtin_amdgcn_exp2f(d * sl2 - lt2) : 0.0f;
+                pd[u] = pu[u] * dp;
+                dsum += pd[u];
             }
+            // both neighbours at once: v_dot2 over (k_a, k_b) pairs, weights in the input dtype
+            pv2<DT>(A, pd[0], pd[1], klo[0], khi[0], klo[1], khi[1]);
+            pv2<DT>(Bk, pu[0], pu[1], klo[0], khi[0], klo[1], khi[1]);
         }
         const float delta = group_allreduce<LPN, false>(dsum);
         float o8[8];
@@ -220,21 +225,16 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams
                 ld16<DT>(gb, uint32_t(t[u]) * grow + loff, glo[u], ghi[u]);
                 st[u] = rs[t[u]];
             }
+            float pu[2], ds[2];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float d = group_sum<LPN>(dot8<DT>(qlo[u], qhi[u], klo, khi));
                 const float dp = group_sum<LPN>(dot8<DT>(glo[u], ghi[u], vlo, vhi));
-                const float pu = en[u] < e1 ? exp2f(d * sl2 - st[u].x) : 0.0f;
-                const float ds = pu * (dp - st[u].y);
-                float qf[8], gf[8];
-                cvt8<DT>(qlo[u], qhi[u], qf);
-                cvt8<DT>(glo[u], ghi[u], gf);
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    ak[c] = fmaf(ds, qf[c], ak[c]);
-                    av[c] = fmaf(pu, gf[c], av[c]);
-                }
+                pu[u] = en[u] < e1 ? __builtin_amdgcn_exp2f(d * sl2 - st[u].x) : 0.0f;
+                ds[u] = pu[u] * (dp - st[u].y);
             }
+            pv2<DT>(ak, ds[0], ds[1], qlo[0], qhi[0], qlo[1], qhi[1]);
+            pv2<DT>(av, pu[0], pu[1], glo[0], ghi[0], glo[1], ghi[1]);
         }
         float ok8[8], ov8[8];
 #pragma unroll
@@ -260,34 +260,28 @@ int key_bits(int64_t B, int64_t T)
 }
 
 struct BwdLayout {
-    size_t counts, off, keys, keys_out, vals, vals_out, row_stats, scan_tmp, sort_tmp, total;
-    size_t scan_bytes, sort_bytes;
+    size_t off, keys, keys_out, vals, vals_out, row_stats, sort_tmp, total;
+    size_t sort_bytes;
 };
 
 hipError_t bwd_layout(int64_t B, int64_t H, int64_t T, int64_t K, BwdLayout& L)
 {
     const size_t nkeys = size_t(B * T) + 1;
     const size_t n = size_t(B * T * K);
-    L.scan_bytes = 0;
     L.sort_bytes = 0;
-    hipError_t e = rocprim::exclusive_scan(nullptr, L.scan_bytes, static_cast<const uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr), 0u, nkeys,
-                                           rocprim::plus<uint32_t>(), hipStream_t(0));
-    if (e != hipSuccess) return e;
-    e = rocprim::radix_sort_pairs(nullptr, L.sort_bytes, static_cast<const uint32_t*>(nullptr),
-                                  static_cast<uint32_t*>(nullptr), static_cast<const uint32_t*>(nullptr),
-                                  static_cast<uint32_t*>(nullptr), n, 0, key_bits(B, T), hipStream_t(0));
+    const hipError_t e = rocprim::radix_sort_pairs(
+        nullptr, L.sort_bytes, static_cast<const uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr),
+        static_cast<const uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr), n, 0, key_bits(B, T),
+        hipStream_t(0));
     if (e != hipSuccess) return e;
     size_t o = 0;
-    L.counts = o;   o += a256(nkeys * 4);
-    L.off = o;      o += a256(nkeys * 4);
-    L.keys = o;     o += a256(n * 4);
-    L.keys_out = o; o += a256(n * 4);
-    L.vals = o;     o += a256(n * 4);
-    L.vals_out = o; o += a256(n * 4);
+    L.off = o;       o += a256(nkeys * 4);
+    L.keys = o;      o += a256(n * 4);
+    L.keys_out = o;  o += a256(n * 4);
+    L.vals = o;      o += a256(n * 4);
+    L.vals_out = o;  o += a256(n * 4);
     L.row_stats = o; o += a256(size_t(B * H * T) * 8);
-    L.scan_tmp = o; o += a256(L.scan_bytes);
-    L.sort_tmp = o; o += a256(L.sort_bytes);
+    L.sort_tmp = o;  o += a256(L.sort_bytes);
     L.total = o;
     return hipSuccess;
 }
@@ -327,7 +321,6 @@ hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, si
     if (e != hipSuccess) return e;
     if (ws_bytes < L.total) return hipErrorInvalidValue;
     char* w = static_cast<char*>(ws);
-    uint32_t* counts = reinterpret_cast<uint32_t*>(w + L.counts);
     uint32_t* off = reinterpret_cast<uint32_t*>(w + L.off);
     uint32_t* keys = reinterpret_cast<uint32_t*>(w + L.keys);
     uint32_t* keys_out = reinterpret_cast<uint32_t*>(w + L.keys_out);
@@ -336,21 +329,19 @@ hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, si
     const int64_t nkeys = p.B * p.T + 1;
     const int64_t n = p.B * p.T * p.K;
 
-    // counts start at zero: a fill kernel rather than a memset node (graph-capture safe)
-    fill_u32<<<dim3(unsigned((nkeys + 255) / 256)), dim3(256), 0, s>>>(counts, nkeys, 0u);
     bwd_transpose_keys<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(
         p.idx, p.is[0], p.is[1], p.is[2], uint32_t(p.B), uint32_t(p.T), uint32_t(p.K),
-        (p.flags & 1u) != 0, keys, vals, counts);
+        (p.flags & 1u) != 0, keys, vals);
     e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    size_t scan_bytes = L.scan_bytes;
-    e = rocprim::exclusive_scan(static_cast<void*>(w + L.scan_tmp), scan_bytes, static_cast<const uint32_t*>(counts),
-                                off, 0u, size_t(nkeys), rocprim::plus<uint32_t>(), s);
     if (e != hipSuccess) return e;
     size_t sort_bytes = L.sort_bytes;
     e = rocprim::radix_sort_pairs(static_cast<void*>(w + L.sort_tmp), sort_bytes, static_cast<const uint32_t*>(keys),
                                   keys_out, static_cast<const uint32_t*>(vals), vals_out, size_t(n), 0,
                                   key_bits(p.B, p.T), s);
+    if (e != hipSuccess) return e;
+    bwd_list_offsets<<<dim3(unsigned((nkeys + 255) / 256)), dim3(256), 0, s>>>(keys_out, uint32_t(n),
+                                                                             uint32_t(nkeys), off);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     p.row_stats = reinterpret_cast<float2*>(w + L.row_stats);
     p.off = off;
