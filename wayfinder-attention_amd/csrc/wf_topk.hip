@@ -254,6 +254,21 @@ __device__ __forceinline__ uint64_t xor16_u64(uint64_t x, int u)
     }
 }
 
+// value of lane u ^ lx within the 16-lane row, lx in {1, 2, 3, 4, 7, 8, 15} (a compile-time
+// constant once the caller's loops unroll)
+__device__ __forceinline__ uint64_t lane_xor16_u64(uint64_t x, int lx, int u)
+{
+    switch (lx) {
+    case 1: return xor16_u64<1>(x, u);
+    case 2: return xor16_u64<2>(x, u);
+    case 3: return dpp64<0x1B>(x);       // quad_perm [3,2,1,0]
+    case 4: return xor16_u64<4>(x, u);
+    case 7: return dpp64<0x141>(x);      // row_half_mirror
+    case 8: return xor16_u64<8>(x, u);
+    default: return dpp64<0x140>(x);     // row_mirror: lane 15 - u
+    }
+}
+
 struct Entry {
     float s;      // MFMA score while pending, exact score after rescoring
     uint32_t j;   // key index
@@ -525,35 +540,38 @@ __device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
         const uint2 en = reinterpret_cast<const uint2*>(pool)[i];
         key[m] = i < kept ? make_key(__uint_as_float(en.x), en.y) : 0ull;
     }
+    // Bitonic sort into descending order in which every compare-exchange has the same
+    // direction: the first step of each merge pairs element i with its mirror i ^ (kk - 1)
+    // inside the 2S-block, the following steps pair i with i ^ jj; the lower element index
+    // keeps the larger key. Partners inside the lane are registers; across lanes they are
+    // one DPP move (mirror: lane u ^ 1/3/7/15 and element EPL-1-m; xor: u ^ 1/2/4/8).
 #pragma unroll
     for (int kk = 2; kk <= KP2; kk <<= 1) {
 #pragma unroll
         for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-            if (jj < EPL) {
+            const bool mirror = jj == (kk >> 1);
+            const int x = mirror ? kk - 1 : jj;   // partner index = i ^ x
+            if (x < EPL) {
 #pragma unroll
                 for (int m = 0; m < EPL; ++m) {
-                    if (m & jj) continue;
-                    const int m2 = m | jj;
-                    const bool desc = ((u * EPL + m) & kk) == 0;
+                    const int m2 = m ^ x;
+                    if (m2 <= m) continue;
                     const uint64_t a = key[m], b = key[m2];
-                    const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
-                    key[m] = desc ? hi : lo;
-                    key[m2] = desc ? lo : hi;
+                    const bool gt = a > b;
+                    key[m] = gt ? a : b;
+                    key[m2] = gt ? b : a;
                 }
             } else {
-                const int lx = jj / EPL;   // folds to a constant once the loops unroll
+                const int lx = x / EPL;                           // partner lane = u ^ lx
+                const int hb = mirror ? (kk / EPL) >> 1 : lx;     // lane bit of the pair's top index bit
+                const bool keep_max = (u & hb) == 0;
+                uint64_t other[EPL];
+#pragma unroll
+                for (int m = 0; m < EPL; ++m) other[m] = lane_xor16_u64(key[mirror ? EPL - 1 - m : m], lx, u);
 #pragma unroll
                 for (int m = 0; m < EPL; ++m) {
-                    const int i = u * EPL + m;
-                    const uint64_t other = lx == 1 ? xor16_u64<1>(key[m], u)
-                                         : lx == 2 ? xor16_u64<2>(key[m], u)
-                                         : lx == 4 ? xor16_u64<4>(key[m], u)
-                                                   : xor16_u64<8>(key[m], u);
-                    const bool low = (i & jj) == 0;
-                    const bool desc = (i & kk) == 0;
-                    const uint64_t hi = key[m] > other ? key[m] : other;
-                    const uint64_t lo = key[m] > other ? other : key[m];
-                    key[m] = (low == desc) ? hi : lo;
+                    const bool gt = key[m] > other[m];
+                    key[m] = gt == keep_max ? key[m] : other[m];
                 }
             }
         }
@@ -568,7 +586,7 @@ __device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
             oi[i] = int32_t(0xffffffffu - uint32_t(key[m]));
             if (os) os[i] = unord_f32(uint32_t(key[m] >> 32));
         } else {
-            oi[i] = int32_t((row + k_eff + i + 1) % T);
+            oi[i] = int32_t((uint32_t(row) + uint32_t(k_eff) + uint32_t(i) + 1u) % uint32_t(T));   // < 2^32: T < 2^31
             if (os) os[i] = -__builtin_inff();
         }
     }
