@@ -185,11 +185,16 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 // [0, T) (they come from this library's retrieval), so the wrap/clamp is skipped.
 // Byte offsets of gathered rows use 24-bit multiplies (T and the row strides below 2^24,
 // checked by the host).
-template <typename DT, int D, int NB, bool LSE, bool TRUST>
+// VI: lane group g takes the NB consecutive slots g*NB .. g*NB+NB-1 of a task, so its
+// indices arrive in one 16-byte load per task instead of one 4-byte load per step (a quarter
+// of the vector-memory instructions, which all pay the same texture-address cost); needs
+// K % 4 == 0, 16-byte aligned index rows and K >= NB (checked by the launcher).
+template <typename DT, int D, int NB, bool LSE, bool TRUST, bool VI>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(sizeof(DT) == 2 && !LSE ? 4 : 1)))
 void sparse_readout_fast(ReadoutParams p)
 {
     static_assert(NB % 2 == 0, "steps are consumed in pairs");
+    static_assert(!VI || NB == 4, "one 16-byte index load per task");
     constexpr int LPN = D / 8;
     constexpr int NPS = 64 / LPN;
     constexpr int CH = NB * NPS;
@@ -236,10 +241,22 @@ void sparse_readout_fast(ReadoutParams p)
     int ri = 0, qi = 0;   // task of stage I
     auto fetch_idx = [&]() {
         const char* ip = reinterpret_cast<const char*>(ib + ri * irow);
+        int jv[NB];
+        if constexpr (VI) {
+            // slots past K (masked in the compute) read the row's last NB indices instead
+            const int s0 = min(qi * CH + grp * NB, K - NB);
+            const uint4 w = *reinterpret_cast<const uint4*>(ip + uint32_t(s0) * 4u);
+            jv[0] = int(w.x); jv[1] = int(w.y); jv[2] = int(w.z); jv[3] = int(w.w);
+        } else {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int slot = min(qi * CH + u * NPS + grp, K - 1);
+                jv[u] = *reinterpret_cast<const int*>(ip + uint32_t(slot) * 4u);
+            }
+        }
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            const int slot = min(qi * CH + u * NPS + grp, K - 1);
-            int j = *reinterpret_cast<const int*>(ip + uint32_t(slot) * 4u);
+            int j = jv[u];
             if constexpr (!TRUST) {
                 j += (j >> 31) & T;
                 j = min(max(j, 0), T - 1);
@@ -268,7 +285,8 @@ void sparse_readout_fast(ReadoutParams p)
             for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
         }
         const int t = int(tw) + rc;
-        const int slot0 = qc * CH + grp;
+        const int slot0 = qc * CH + (VI ? grp * NB : grp);   // slot of step u: slot0 + u * SU
+        constexpr int SU = VI ? 1 : NPS;
         const int lim = (mask_flag && t < K - 1) ? t + 1 : K;   // slots >= lim carry no weight
         float sc[NB];
         float bm = -__builtin_inff();
@@ -282,7 +300,7 @@ void sparse_readout_fast(ReadoutParams p)
 #pragma unroll
             for (int u = 0; u < NB; ++u) {
                 const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
-                sc[u] = slot0 + u * NPS < lim ? d * sl2 : -__builtin_inff();
+                sc[u] = slot0 + u * SU < lim ? d * sl2 : -__builtin_inff();
                 bm = fmaxf(bm, sc[u]);
             }
         }
@@ -358,11 +376,22 @@ hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
 #ifndef WF_READOUT_FAST_NB
 #define WF_READOUT_FAST_NB 4
 #endif
+    constexpr int NB = WF_READOUT_FAST_NB;
     const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
     const dim3 g(static_cast<unsigned>(grid)), blk(64 * kWaves);
-    if (p.lse2) sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, true, false><<<g, blk, 0, s>>>(p);
-    else if (p.flags & kFlagTrustedIndices) sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, false, true><<<g, blk, 0, s>>>(p);
-    else sparse_readout_fast<DT, D, WF_READOUT_FAST_NB, false, false><<<g, blk, 0, s>>>(p);
+    // 16-byte index loads: K a multiple of 4 (row starts stay 16-byte aligned given an
+    // aligned base and row strides that are multiples of 4)
+    const bool vi = NB == 4 && p.K % 4 == 0 && p.K >= NB && reinterpret_cast<uintptr_t>(p.idx) % 16 == 0 &&
+                    p.is[0] % 4 == 0 && p.is[1] % 4 == 0;
+    if (vi) {
+        if (p.lse2) sparse_readout_fast<DT, D, NB, true, false, true><<<g, blk, 0, s>>>(p);
+        else if (p.flags & kFlagTrustedIndices) sparse_readout_fast<DT, D, NB, false, true, true><<<g, blk, 0, s>>>(p);
+        else sparse_readout_fast<DT, D, NB, false, false, true><<<g, blk, 0, s>>>(p);
+    } else {
+        if (p.lse2) sparse_readout_fast<DT, D, NB, true, false, false><<<g, blk, 0, s>>>(p);
+        else if (p.flags & kFlagTrustedIndices) sparse_readout_fast<DT, D, NB, false, true, false><<<g, blk, 0, s>>>(p);
+        else sparse_readout_fast<DT, D, NB, false, false, false><<<g, blk, 0, s>>>(p);
+    }
     return hipGetLastError();
 }
 
