@@ -222,7 +222,25 @@ def bench_decoder(args):
     ms = time_loop(step, args.steps, args.warmup)
     peak_mb = (torch.cuda.max_memory_allocated() - base) / 2 ** 20
     med, mn, p90 = per_call_ms(step, max(10, args.steps // 2))
+    # the same forward captured once as a HIP graph and replayed (serving loops): the
+    # launches of the ~60 kernels per forward go out as one graph launch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    gms = time_loop(graph.replay, args.steps, args.warmup)
     dms = time_loop(dense_step, args.steps, args.warmup)
+    dgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        dense_step()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(dgraph):
+        dense_step()
+    dgms = time_loop(dgraph.replay, args.steps, args.warmup)
     tokens = c["B"] * c["T"]
     line = {
         "metric": "config-2 4-layer learned-address decoder forward throughput (tokens/s)",
@@ -235,7 +253,10 @@ def bench_decoder(args):
         "latency_ms": {"mean": round(ms, 4), "median": round(med, 4), "min": round(mn, 4),
                        "p90": round(p90, 4)},
         "peak_mb": round(peak_mb, 1),
+        "graph_replay_ms_per_step": round(gms, 4),
+        "graph_replay_tokens_per_s": round(tokens / (gms * 1e-3), 1),
         "dense_causal_sdpa_decoder_ms": round(dms, 4),
+        "dense_graph_replay_ms": round(dgms, 4),
         "vs_dense": round(dms / ms, 3),
     }
     print(json.dumps(line), flush=True)
