@@ -165,6 +165,7 @@ bool readout_rows(wf::ReadoutParams& p, int64_t r0, int64_t r1)
     p.rows_per_seg = cdiv(r1 - r0, p.seg_per_pair);
     p.vpairs = nbh * p.seg_per_pair;
     p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
+    p.head_major = p.vpairs * p.wg_per_vpair > wf::kReadoutResidentWGs ? 1 : 0;
     return p.vpairs * p.wg_per_vpair < (int64_t(1) << 31);
 }
 

@@ -128,10 +128,14 @@ struct ReadoutParams {
     int64_t rows_per_seg;
     int64_t vpairs;         // B*H*seg_per_pair virtual pairs
     int64_t wg_per_vpair;   // workgroups per virtual pair
+    int head_major;         // workgroup order: 1 = virtual pair by virtual pair (grids larger
+                            // than one residency wave), 0 = pair blockIdx % 8 (one wave)
 };
 
-// Backward of the readout (fixed indices). Both passes use the forward's XCD-aware mapping:
-// the row pass over query rows t, the key pass over key rows j, of one (b, h) pair per XCD.
+// Backward of the readout (fixed indices). Both passes pair blockIdx % 8 with a fixed set of
+// (b, h) pairs at every grid size (the row pass over query rows t, the key pass over key rows
+// j): chunk-major order starts the key pass's long early-key lists of every pair first, which
+// measured 27 % faster than running the pairs one after another.
 struct ReadoutBwdParams {
     const void* q;
     const void* k;
@@ -179,6 +183,9 @@ constexpr unsigned kFlagTrustedIndices = 0x80000000u;
 constexpr int kAbsmaxChunk = 256;
 // Query rows per readout workgroup (4 waves x 4 consecutive rows).
 constexpr int kReadoutRowsPerWG = 16;
+// Readout workgroups resident at once on MI355X (256 CUs x 4 workgroups of 4 waves at the
+// fast kernel's 4 waves per SIMD): grids above this run in several residency waves.
+constexpr int64_t kReadoutResidentWGs = 1024;
 
 // launchers (return hipError_t of the launch)
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
