@@ -86,6 +86,15 @@ def test_workspace_size(lib):
     assert lib.wf_causal_topk_workspace_bytes(4, 65536, 32, 256) == 4 * 256 * 4
     assert lib.wf_causal_topk_workspace_bytes(0, 10, 32, 8) == 0
     assert lib.wf_fused_workspace_bytes(2, 1000, 32, 8) == lib.wf_causal_topk_workspace_bytes(2, 1000, 32, 8)
+    # backward workspace: a pure function of the shape (no device query): offsets, two
+    # ping-pong (key, row) arrays, row stats, radix histograms (256 per 4096-slot tile), totals
+    a256 = lambda x: (x + 255) // 256 * 256
+    for B, H, T, K in ((1, 8, 16384, 128), (2, 3, 300, 7)):
+        n = B * T * K
+        want = (a256((B * T + 1) * 4) + 4 * a256(n * 4) + a256(B * H * T * 8)
+                + a256(256 * ((n + 4095) // 4096) * 4) + a256(256 * 4))
+        assert lib.wf_sparse_readout_bwd_workspace_bytes(B, H, T, K) == want
+    assert lib.wf_sparse_readout_bwd_workspace_bytes(1, 1, 0, 4) == 0
 
 
 def _readout(lib, **kw):

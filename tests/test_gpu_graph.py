@@ -3,8 +3,9 @@ decoder are captured once with torch.cuda.graph and replayed several times, with
 inputs copied into the captured buffers and eager calls of the same path between the
 replays; every replay must equal the eager result bit for bit (both paths are
 deterministic: the retrieval writes indices in canonical order and the readout has no
-atomics). Nothing on these paths issues a memset, so the captured graph holds kernel
-nodes only."""
+atomics). The readout backward (index transpose by its own radix passes, row and key
+passes) is captured the same way. Nothing on these paths issues a memset, so the captured
+graphs hold kernel nodes only."""
 
 from __future__ import annotations
 
@@ -14,6 +15,7 @@ import pytest
 import torch
 
 from routing_attention.kernels import fused_sparse_attention
+from routing_attention.kernels.sparse_autograd import readout_bwd, readout_fwd_lse
 from routing_attention.models import TransformerLM
 from tests.helpers import addresses, qkv
 
@@ -88,3 +90,34 @@ def test_decoder_forward_graph_replays(device):
         e_logits = fwd()
         torch.cuda.synchronize()
         assert torch.equal(g_logits, e_logits), f"replay {rep}: logits differ"
+
+
+def test_readout_backward_graph_replays(device):
+    B, H, T, D, R, K = 1, 4, 2048, 64, 32, 64
+    _say(f"[graph] readout backward B={B} H={H} T={T} D={D} K={K} bf16")
+    dt = torch.bfloat16
+    scale = D ** -0.5
+    sets = []
+    for seed in (21, 22):
+        qa, ka = addresses(B, T, R, seed=seed)
+        idx = fused_sparse_attention(qa.to(dt).to(device), ka.to(dt).to(device),
+                                     *[t.to(dt).to(device) for t in qkv(B, H, T, D, seed=seed)],
+                                     K, scale)[1]
+        q, k, v = (t.to(dt).to(device) for t in qkv(B, H, T, D, seed=seed + 200))
+        _, lse2 = readout_fwd_lse(q, k, v, idx, scale)
+        dout = torch.randn(B, H, T, D, generator=torch.Generator().manual_seed(seed)).to(dt).to(device)
+        sets.append([q, k, v, idx, lse2, dout])
+    static = [t.clone() for t in sets[0]]
+
+    def bwd():
+        return readout_bwd(*static, scale)
+
+    g, g_grads = _capture(bwd)
+    for rep in range(4):
+        for s_, src in zip(static, sets[rep % 2]):
+            s_.copy_(src)
+        g.replay()
+        e_grads = bwd()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("dq", "dk", "dv"), g_grads, e_grads):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs"

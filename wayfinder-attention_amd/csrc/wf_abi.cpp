@@ -282,10 +282,7 @@ int wf_sparse_readout_fwd_lse(const void* q, const void* k, const void* v, int d
 size_t wf_sparse_readout_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K)
 {
     if (B <= 0 || H <= 0 || T <= 0 || K <= 0) return 0;
-    hipError_t e = hipSuccess;
-    const size_t n = wf::sparse_readout_bwd_workspace(B, H, T, K, &e);
-    if (e != hipSuccess) fail(WF_ERR_HIP, "sparse_readout_bwd: workspace sizing: %s", hipGetErrorString(e));
-    return n;
+    return wf::sparse_readout_bwd_workspace(B, H, T, K);
 }
 
 int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
@@ -313,9 +310,7 @@ int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
                                         "16-byte aligned rows and a per-(b,h) span below 4 GiB");
     if (a->idx_strides[2] != 1)
         return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: index rows must be contiguous (idx_strides[2] == 1)");
-    hipError_t e = hipSuccess;
-    const size_t need = wf::sparse_readout_bwd_workspace(B, H, T, K, &e);
-    if (e != hipSuccess) return hip_fail("sparse_readout_bwd: workspace sizing", e);
+    const size_t need = wf::sparse_readout_bwd_workspace(B, H, T, K);
     if (!a->workspace || a->workspace_bytes < need)
         return fail(WF_ERR_WORKSPACE, "sparse_readout_bwd: workspace of %zu bytes required, got %zu", need,
                     a->workspace ? a->workspace_bytes : size_t(0));
@@ -342,7 +337,8 @@ int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
     p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
     if (p.vpairs * p.wg_per_vpair >= (int64_t(1) << 31))
         return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: problem too large for one launch");
-    e = wf::launch_sparse_readout_bwd(dt, p, a->workspace, a->workspace_bytes, static_cast<hipStream_t>(stream));
+    const hipError_t e = wf::launch_sparse_readout_bwd(dt, p, a->workspace, a->workspace_bytes,
+                                                       static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail("sparse_readout_bwd: launch", e);
     return ok();
 }

@@ -191,9 +191,9 @@ constexpr int64_t kReadoutResidentWGs = 1024;
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutParams& p, hipStream_t s);
-// device workspace of the backward for this shape (index transpose, per-row deltas and the
-// rocPRIM scan / sort scratch); 0 with *err set when rocPRIM cannot size it
-size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K, hipError_t* err);
+// device workspace of the backward for this shape (index transpose arrays, radix histograms,
+// per-row statistics); a function of the shape only
+size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K);
 hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_address_project(int dtype, const AddressParams& p, hipStream_t s);
 

@@ -11,10 +11,12 @@
 //   dv_j = sum_{(t,s): j_s = j} p_s dout_t
 //
 // computed without floating-point atomics, so the gradients are deterministic:
-//  1. index transpose: a stable rocPRIM radix sort of (b*T + j) keys with the query row t
-//     as value groups the rows that selected each key, t ascending; a binary search per key
-//     over the sorted keys gives each list's offset. Masked pad slots sort past the last
-//     list.
+//  1. index transpose: a stable LSD radix sort (8-bit digits; per pass a workgroup
+//     histogram, a per-digit scan over workgroups and a stable scatter ranked with wave
+//     ballots) of (b*T + j) keys with the query row t as value groups the rows that selected
+//     each key, t ascending; a binary search per key over the sorted keys gives each list's
+//     offset. Masked pad slots sort past the last list. No memsets, no global atomics: every
+//     count is written whole, so the backward can be captured into a HIP graph.
 //  2. row pass (the forward's mapping: one wave walks 4 query rows, D/8 lanes per
 //     neighbour): recomputes p from the forward's base-2 log-sum-exp and writes dq, and
 //     (lse2, delta) per row for the key pass -- delta exact, from the row's own p and dp
@@ -23,34 +25,154 @@
 //     dout_t -- the forward's access pattern with the roles of query and key swapped -- and
 //     recomputes p and dp for every entry. Nothing of size (B, H, T, K) is stored.
 // All accumulation is fp32; each gradient element is rounded once to the input dtype.
-#include <rocprim/device/device_radix_sort.hpp>
-
 #include "wf_readout_dev.h"
 
 namespace wf {
 namespace {
 
-// One thread per (b, t, s) slot: key b*T + j (j wrapped and clamped as in the forward),
-// value t. Masked pad slots (s > t on rows t < K-1 with WF_FLAG_MASK_PADS) carry no weight:
-// they get the key B*T, which sorts past every list. B*T*K < 2^32 (checked by the entry
-// point), so the slot arithmetic is 32-bit.
-__global__ void bwd_transpose_keys(const int32_t* idx, int64_t is0, int64_t is1, int64_t is2,
-                                   uint32_t B, uint32_t T, uint32_t K, bool mask_pads,
-                                   uint32_t* keys, uint32_t* vals)
+// ---------------------------------------------------------------- index transpose
+constexpr int kSortThreads = 256;                      // 4 waves
+constexpr int kSortItems = 16;                         // items per thread and pass
+constexpr uint32_t kSortTile = kSortThreads * kSortItems;
+
+// Input of one radix pass: the (b, t, s) slots themselves on the first pass (key b*T + j with
+// j wrapped and clamped as in the forward, value t; masked pad slots -- s > t on rows
+// t < K-1 with WF_FLAG_MASK_PADS -- get the key B*T, past every list), the previous pass's
+// arrays after it. B*T*K < 2^32 (checked by the entry point), so slot arithmetic is 32-bit.
+struct SortSrc {
+    const int32_t* idx;
+    int64_t is0, is1, is2;
+    uint32_t B, T, K;
+    bool mask_pads;
+    const uint32_t* keys;   // null: first pass
+    const uint32_t* vals;
+};
+
+__device__ __forceinline__ uint32_t sort_key(const SortSrc& s, uint32_t e, uint32_t& val)
 {
-    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t TK = T * K;
-    if (e >= B * TK) return;
+    if (s.keys) {
+        val = s.vals[e];
+        return s.keys[e];
+    }
+    const uint32_t TK = s.T * s.K;
     const uint32_t b = e / TK;
     const uint32_t r = e - b * TK;
-    const uint32_t t = r / K;
-    const uint32_t s = r - t * K;
-    int j = idx[int64_t(b) * is0 + int64_t(t) * is1 + int64_t(s) * is2];
-    j += (j >> 31) & int(T);
-    j = min(max(j, 0), int(T) - 1);
-    const bool masked = mask_pads && t + 1 < K && s > t;
-    keys[e] = masked ? B * T : b * T + uint32_t(j);
-    vals[e] = t;
+    const uint32_t t = r / s.K;
+    const uint32_t sl = r - t * s.K;
+    int j = s.idx[int64_t(b) * s.is0 + int64_t(t) * s.is1 + int64_t(sl) * s.is2];
+    j += (j >> 31) & int(s.T);
+    j = min(max(j, 0), int(s.T) - 1);
+    val = t;
+    const bool masked = s.mask_pads && t + 1 < s.K && sl > t;
+    return masked ? s.B * s.T : b * s.T + uint32_t(j);
+}
+
+// Digit histogram of one tile: H[d * nblk + tile] = items of the tile with digit d.
+__global__ __launch_bounds__(kSortThreads) void radix_hist(SortSrc s, uint32_t n, int shift,
+                                                           uint32_t nblk, uint32_t* H)
+{
+    __shared__ uint32_t h[256];
+    const uint32_t tid = threadIdx.x;
+    h[tid] = 0;
+    __syncthreads();
+    for (int i = 0; i < kSortItems; ++i) {
+        const uint32_t e = blockIdx.x * kSortTile + uint32_t(i) * kSortThreads + tid;
+        if (e < n) {
+            uint32_t v;
+            atomicAdd(&h[(sort_key(s, e, v) >> shift) & 255u], 1u);
+        }
+    }
+    __syncthreads();
+    H[tid * nblk + blockIdx.x] = h[tid];
+}
+
+// Exclusive scan of 256 values across the workgroup (one per thread); returns the exclusive
+// prefix of this thread's value, and the total in *sum.
+__device__ __forceinline__ uint32_t block_excl_scan256(uint32_t x, uint32_t* buf, uint32_t* sum)
+{
+    const uint32_t tid = threadIdx.x;
+    buf[tid] = x;
+    for (uint32_t o = 1; o < 256; o <<= 1) {
+        __syncthreads();
+        const uint32_t y = tid >= o ? buf[tid - o] : 0u;
+        __syncthreads();
+        buf[tid] += y;
+    }
+    __syncthreads();
+    *sum = buf[255];
+    const uint32_t incl = buf[tid];
+    __syncthreads();
+    return incl - x;
+}
+
+// One workgroup per digit d: H[d][*] becomes its exclusive scan over tiles, total[d] the
+// digit's count.
+__global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* H, uint32_t nblk, uint32_t* total)
+{
+    __shared__ uint32_t buf[256];
+    uint32_t* row = H + size_t(blockIdx.x) * nblk;
+    const uint32_t per = (nblk + kSortThreads - 1) / kSortThreads;
+    const uint32_t beg = min(threadIdx.x * per, nblk), end = min(beg + per, nblk);
+    uint32_t sum = 0;
+    for (uint32_t i = beg; i < end; ++i) sum += row[i];
+    uint32_t all;
+    uint32_t run = block_excl_scan256(sum, buf, &all);
+    for (uint32_t i = beg; i < end; ++i) {
+        const uint32_t v = row[i];
+        row[i] = run;
+        run += v;
+    }
+    if (threadIdx.x == 0) total[blockIdx.x] = all;
+}
+
+// Stable scatter of one tile: items are taken in order (round r, thread t -> item
+// tile*kSortTile + r*256 + t); an item's place among the tile's items of its digit is the
+// count in earlier rounds + in earlier waves of this round + in earlier lanes of its wave
+// (lanes with the same digit found by 8 ballots).
+__global__ __launch_bounds__(kSortThreads) void radix_scatter(SortSrc s, uint32_t n, int shift,
+                                                              uint32_t nblk, const uint32_t* H,
+                                                              const uint32_t* total,
+                                                              uint32_t* okeys, uint32_t* ovals)
+{
+    __shared__ uint32_t buf[256], base[256], run[256], wcnt[4][256];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, w = tid >> 6;
+    uint32_t all;
+    const uint32_t pre = block_excl_scan256(total[tid], buf, &all);
+    base[tid] = pre + H[tid * nblk + blockIdx.x];
+    run[tid] = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wcnt[k][tid] = 0;
+    __syncthreads();
+    const uint64_t lt = (uint64_t(1) << lane) - 1;
+    for (int r = 0; r < kSortItems; ++r) {
+        const uint32_t e = blockIdx.x * kSortTile + uint32_t(r) * kSortThreads + tid;
+        const bool valid = e < n;
+        uint32_t key = 0, val = 0;
+        if (valid) key = sort_key(s, e, val);
+        const uint32_t d = (key >> shift) & 255u;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+            const bool on = (d >> bit) & 1u;
+            const uint64_t m = __ballot(on);
+            peers &= on ? m : ~m;
+        }
+        const uint32_t rank = __popcll(peers & lt);
+        if (valid && rank == 0) wcnt[w][d] = __popcll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t off = run[d] + rank;
+            for (uint32_t k = 0; k < w; ++k) off += wcnt[k][d];
+            okeys[base[d] + off] = key;
+            ovals[base[d] + off] = val;
+        }
+        __syncthreads();
+        run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wcnt[k][tid] = 0;
+        __syncthreads();
+    }
 }
 
 // off[k] = first position of the sorted keys holding a key >= k, for k = 0 .. B*T: the start
@@ -260,20 +382,16 @@ int key_bits(int64_t B, int64_t T)
 }
 
 struct BwdLayout {
-    size_t off, keys, keys_out, vals, vals_out, row_stats, sort_tmp, total;
-    size_t sort_bytes;
+    size_t off, keys, keys_out, vals, vals_out, row_stats, hist, total, total_bytes;
+    uint32_t nblk;
 };
 
-hipError_t bwd_layout(int64_t B, int64_t H, int64_t T, int64_t K, BwdLayout& L)
+BwdLayout bwd_layout(int64_t B, int64_t H, int64_t T, int64_t K)
 {
+    BwdLayout L{};
     const size_t nkeys = size_t(B * T) + 1;
     const size_t n = size_t(B * T * K);
-    L.sort_bytes = 0;
-    const hipError_t e = rocprim::radix_sort_pairs(
-        nullptr, L.sort_bytes, static_cast<const uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr),
-        static_cast<const uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr), n, 0, key_bits(B, T),
-        hipStream_t(0));
-    if (e != hipSuccess) return e;
+    L.nblk = uint32_t((n + kSortTile - 1) / kSortTile);
     size_t o = 0;
     L.off = o;       o += a256(nkeys * 4);
     L.keys = o;      o += a256(n * 4);
@@ -281,9 +399,10 @@ hipError_t bwd_layout(int64_t B, int64_t H, int64_t T, int64_t K, BwdLayout& L)
     L.vals = o;      o += a256(n * 4);
     L.vals_out = o;  o += a256(n * 4);
     L.row_stats = o; o += a256(size_t(B * H * T) * 8);
-    L.sort_tmp = o;  o += a256(L.sort_bytes);
-    L.total = o;
-    return hipSuccess;
+    L.hist = o;      o += a256(size_t(256) * L.nblk * 4);
+    L.total = o;     o += a256(256 * 4);
+    L.total_bytes = o;
+    return L;
 }
 
 template <typename DT>
@@ -306,46 +425,48 @@ hipError_t launch_passes(const ReadoutBwdParams& p, hipStream_t s)
 
 }  // namespace
 
-size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K, hipError_t* err)
+size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K)
 {
-    BwdLayout L{};
-    const hipError_t e = bwd_layout(B, H, T, K, L);
-    if (err) *err = e;
-    return e == hipSuccess ? L.total : 0;
+    return bwd_layout(B, H, T, K).total_bytes;
 }
 
 hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s)
 {
-    BwdLayout L{};
-    hipError_t e = bwd_layout(p.B, p.H, p.T, p.K, L);
-    if (e != hipSuccess) return e;
-    if (ws_bytes < L.total) return hipErrorInvalidValue;
+    const BwdLayout L = bwd_layout(p.B, p.H, p.T, p.K);
+    if (ws_bytes < L.total_bytes) return hipErrorInvalidValue;
     char* w = static_cast<char*>(ws);
     uint32_t* off = reinterpret_cast<uint32_t*>(w + L.off);
-    uint32_t* keys = reinterpret_cast<uint32_t*>(w + L.keys);
-    uint32_t* keys_out = reinterpret_cast<uint32_t*>(w + L.keys_out);
-    uint32_t* vals = reinterpret_cast<uint32_t*>(w + L.vals);
-    uint32_t* vals_out = reinterpret_cast<uint32_t*>(w + L.vals_out);
-    const int64_t nkeys = p.B * p.T + 1;
-    const int64_t n = p.B * p.T * p.K;
+    uint32_t* A[2] = {reinterpret_cast<uint32_t*>(w + L.keys), reinterpret_cast<uint32_t*>(w + L.vals)};
+    uint32_t* Z[2] = {reinterpret_cast<uint32_t*>(w + L.keys_out), reinterpret_cast<uint32_t*>(w + L.vals_out)};
+    uint32_t* hist = reinterpret_cast<uint32_t*>(w + L.hist);
+    uint32_t* total = reinterpret_cast<uint32_t*>(w + L.total);
+    const uint32_t nkeys = uint32_t(p.B * p.T + 1);
+    const uint32_t n = uint32_t(p.B * p.T * p.K);
 
-    bwd_transpose_keys<<<dim3(unsigned((n + 255) / 256)), dim3(256), 0, s>>>(
-        p.idx, p.is[0], p.is[1], p.is[2], uint32_t(p.B), uint32_t(p.T), uint32_t(p.K),
-        (p.flags & 1u) != 0, keys, vals);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    size_t sort_bytes = L.sort_bytes;
-    e = rocprim::radix_sort_pairs(static_cast<void*>(w + L.sort_tmp), sort_bytes, static_cast<const uint32_t*>(keys),
-                                  keys_out, static_cast<const uint32_t*>(vals), vals_out, size_t(n), 0,
-                                  key_bits(p.B, p.T), s);
-    if (e != hipSuccess) return e;
-    bwd_list_offsets<<<dim3(unsigned((nkeys + 255) / 256)), dim3(256), 0, s>>>(keys_out, uint32_t(n),
-                                                                             uint32_t(nkeys), off);
-    e = hipGetLastError();
+    if (n > 0) {
+        // 8-bit digits over the key range 0 .. B*T; ping-pong so the last pass lands in Z
+        const int passes = (key_bits(p.B, p.T) + 7) / 8;
+        SortSrc src{p.idx, p.is[0], p.is[1], p.is[2], uint32_t(p.B), uint32_t(p.T), uint32_t(p.K),
+                    (p.flags & 1u) != 0, nullptr, nullptr};
+        for (int pass = 0; pass < passes; ++pass) {
+            uint32_t* const* dst = (passes - 1 - pass) % 2 == 0 ? Z : A;
+            const int shift = 8 * pass;
+            radix_hist<<<dim3(L.nblk), dim3(kSortThreads), 0, s>>>(src, n, shift, L.nblk, hist);
+            radix_scan<<<dim3(256), dim3(kSortThreads), 0, s>>>(hist, L.nblk, total);
+            radix_scatter<<<dim3(L.nblk), dim3(kSortThreads), 0, s>>>(src, n, shift, L.nblk, hist, total,
+                                                                     dst[0], dst[1]);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            src.keys = dst[0];
+            src.vals = dst[1];
+        }
+    }
+    bwd_list_offsets<<<dim3((nkeys + 255) / 256), dim3(256), 0, s>>>(Z[0], n, nkeys, off);
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     p.row_stats = reinterpret_cast<float2*>(w + L.row_stats);
     p.off = off;
-    p.rows = vals_out;
+    p.rows = Z[1];
     if (dtype == 2) return launch_passes<bf16_t>(p, s);
     if (dtype == 1) return launch_passes<_Float16>(p, s);
     return launch_passes<float>(p, s);
