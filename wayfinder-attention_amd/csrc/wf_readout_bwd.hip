@@ -39,10 +39,34 @@ constexpr uint32_t kSortTile = kSortThreads * kSortItems;
 // j wrapped and clamped as in the forward, value t; masked pad slots -- s > t on rows
 // t < K-1 with WF_FLAG_MASK_PADS -- get the key B*T, past every list), the previous pass's
 // arrays after it. B*T*K < 2^32 (checked by the entry point), so slot arithmetic is 32-bit.
+// Unsigned 32-bit division by a divisor fixed per launch (Granlund-Montgomery, round-up
+// multiplier): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, and for every 32-bit x
+// x / d = (t + ((x - t) >> 1)) >> (l - 1) with t = umulhi(x, m); d = 1 is the identity.
+struct FastDiv {
+    uint32_t m, l;
+};
+
+FastDiv make_fastdiv(uint32_t d)
+{
+    FastDiv f{0, 0};
+    if (d <= 1) return f;
+    while ((uint64_t(1) << f.l) < d) ++f.l;
+    f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << f.l) - d)) / d + 1);
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f)
+{
+    if (f.l == 0) return x;
+    const uint32_t t = __umulhi(x, f.m);
+    return (t + ((x - t) >> 1)) >> (f.l - 1);
+}
+
 struct SortSrc {
     const int32_t* idx;
     int64_t is0, is1, is2;
     uint32_t B, T, K;
+    FastDiv divK, divTK;    // by K and by T*K
     bool mask_pads;
     const uint32_t* keys;   // null: first pass
     const uint32_t* vals;
@@ -54,10 +78,9 @@ __device__ __forceinline__ uint32_t sort_key(const SortSrc& s, uint32_t e, uint3
         val = s.vals[e];
         return s.keys[e];
     }
-    const uint32_t TK = s.T * s.K;
-    const uint32_t b = e / TK;
-    const uint32_t r = e - b * TK;
-    const uint32_t t = r / s.K;
+    const uint32_t b = fdiv(e, s.divTK);
+    const uint32_t r = e - b * (s.T * s.K);
+    const uint32_t t = fdiv(r, s.divK);
     const uint32_t sl = r - t * s.K;
     int j = s.idx[int64_t(b) * s.is0 + int64_t(t) * s.is1 + int64_t(sl) * s.is2];
     j += (j >> 31) & int(s.T);
@@ -74,13 +97,18 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist(SortSrc s, uint32_t n
     __shared__ uint32_t h[256];
     const uint32_t tid = threadIdx.x;
     h[tid] = 0;
-    __syncthreads();
+    uint32_t key[kSortItems];   // every load issued before the first use
+#pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
         const uint32_t e = blockIdx.x * kSortTile + uint32_t(i) * kSortThreads + tid;
-        if (e < n) {
-            uint32_t v;
-            atomicAdd(&h[(sort_key(s, e, v) >> shift) & 255u], 1u);
-        }
+        uint32_t v;
+        key[i] = e < n ? sort_key(s, e, v) : 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const uint32_t e = blockIdx.x * kSortTile + uint32_t(i) * kSortThreads + tid;
+        if (e < n) atomicAdd(&h[(key[i] >> shift) & 255u], 1u);
     }
     __syncthreads();
     H[tid * nblk + blockIdx.x] = h[tid];
@@ -128,29 +156,44 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan(uint32_t* H, uint32_t
 // Stable scatter of one tile: items are taken in order (round r, thread t -> item
 // tile*kSortTile + r*256 + t); an item's place among the tile's items of its digit is the
 // count in earlier rounds + in earlier waves of this round + in earlier lanes of its wave
-// (lanes with the same digit found by 8 ballots).
+// (lanes with the same digit found by 8 ballots). The tile is first ordered in LDS by
+// (digit, place), then written out by consecutive threads, so each digit's run of the tile
+// goes to global memory as one contiguous, coalesced stretch.
 __global__ __launch_bounds__(kSortThreads) void radix_scatter(SortSrc s, uint32_t n, int shift,
                                                               uint32_t nblk, const uint32_t* H,
                                                               const uint32_t* total,
                                                               uint32_t* okeys, uint32_t* ovals)
 {
-    __shared__ uint32_t buf[256], base[256], run[256], wcnt[4][256];
+    __shared__ uint32_t buf[256], base[256], lstart[256], run[256], wcnt[4][256];
+    __shared__ uint32_t sk[kSortTile], sv[kSortTile];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, w = tid >> 6;
+    const uint32_t tile0 = blockIdx.x * kSortTile;
+    const uint32_t ntile = min(kSortTile, n - tile0);
+    uint32_t keys[kSortItems], vals[kSortItems];   // every load issued before the rounds
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const uint32_t e = tile0 + uint32_t(r) * kSortThreads + tid;
+        keys[r] = 0;
+        vals[r] = 0;
+        if (e < n) keys[r] = sort_key(s, e, vals[r]);
+    }
+    // digit d of this tile: global start base[d], start inside the tile lstart[d]
+    const uint32_t hd = H[tid * nblk + blockIdx.x];
+    const uint32_t mine = (blockIdx.x + 1 < nblk ? H[tid * nblk + blockIdx.x + 1] : total[tid]) - hd;
     uint32_t all;
     const uint32_t pre = block_excl_scan256(total[tid], buf, &all);
-    base[tid] = pre + H[tid * nblk + blockIdx.x];
+    base[tid] = pre + hd;
+    lstart[tid] = block_excl_scan256(mine, buf, &all);
     run[tid] = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) wcnt[k][tid] = 0;
     __syncthreads();
     const uint64_t lt = (uint64_t(1) << lane) - 1;
+#pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
-        const uint32_t e = blockIdx.x * kSortTile + uint32_t(r) * kSortThreads + tid;
-        const bool valid = e < n;
-        uint32_t key = 0, val = 0;
-        if (valid) key = sort_key(s, e, val);
-        const uint32_t d = (key >> shift) & 255u;
+        const bool valid = uint32_t(r) * kSortThreads + tid < ntile;
+        const uint32_t d = (keys[r] >> shift) & 255u;
         uint64_t peers = __ballot(valid);
 #pragma unroll
         for (int bit = 0; bit < 8; ++bit) {
@@ -162,16 +205,23 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter(SortSrc s, uint32_
         if (valid && rank == 0) wcnt[w][d] = __popcll(peers);
         __syncthreads();
         if (valid) {
-            uint32_t off = run[d] + rank;
+            uint32_t off = lstart[d] + run[d] + rank;
             for (uint32_t k = 0; k < w; ++k) off += wcnt[k][d];
-            okeys[base[d] + off] = key;
-            ovals[base[d] + off] = val;
+            sk[off] = keys[r];
+            sv[off] = vals[r];
         }
         __syncthreads();
         run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
 #pragma unroll
         for (int k = 0; k < 4; ++k) wcnt[k][tid] = 0;
         __syncthreads();
+    }
+    for (uint32_t i = tid; i < ntile; i += kSortThreads) {
+        const uint32_t key = sk[i];
+        const uint32_t d = (key >> shift) & 255u;
+        const uint32_t g = base[d] + (i - lstart[d]);
+        okeys[g] = key;
+        ovals[g] = sv[i];
     }
 }
 
@@ -447,6 +497,7 @@ hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, si
         // 8-bit digits over the key range 0 .. B*T; ping-pong so the last pass lands in Z
         const int passes = (key_bits(p.B, p.T) + 7) / 8;
         SortSrc src{p.idx, p.is[0], p.is[1], p.is[2], uint32_t(p.B), uint32_t(p.T), uint32_t(p.K),
+                    make_fastdiv(uint32_t(p.K)), make_fastdiv(uint32_t(p.T * p.K)),
                     (p.flags & 1u) != 0, nullptr, nullptr};
         for (int pass = 0; pass < passes; ++pass) {
             uint32_t* const* dst = (passes - 1 - pass) % 2 == 0 ? Z : A;
