@@ -183,9 +183,9 @@ constexpr unsigned kFlagTrustedIndices = 0x80000000u;
 constexpr int kAbsmaxChunk = 256;
 // Query rows per readout workgroup (4 waves x 4 consecutive rows).
 constexpr int kReadoutRowsPerWG = 16;
-// Readout workgroups resident at once on MI355X (256 CUs x 4 workgroups of 4 waves at the
-// fast kernel's 4 waves per SIMD): grids above this run in several residency waves.
-constexpr int64_t kReadoutResidentWGs = 1024;
+// Readout workgroups resident at once on MI355X (256 CUs x 5 workgroups of 4 waves at the
+// fast kernel's 5 waves per SIMD): grids above this run in several residency waves.
+constexpr int64_t kReadoutResidentWGs = 1280;
 
 // launchers (return hipError_t of the launch)
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);

@@ -194,17 +194,18 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 // row's tasks; the groups are combined once per row (DPP row_ror within 16-lane rows, two
 // shuffles across rows), so the per-step work has no LDS or ds_bpermute traffic.
 
-// NB (even): wave steps per task. For 16-bit types the allocator is held to 128 registers
-// (4 waves per SIMD; two values spill to scratch): more gathers in flight per CU measured
-// 261 us against 275 us at 3 waves (T=16384, H=8, D=64, bf16).
-// LSE: also write the row's base-2 log-sum-exp (the training forward; it keeps 3 waves per
-// SIMD rather than spill the extra live values). TRUST: the indices are known to lie in
-// [0, T) (they come from this library's retrieval), so the wrap/clamp is skipped.
+// NB (even): wave steps per task. For 16-bit types the allocator is held to at most 128
+// registers (the kernel needs 96: 5 waves per SIMD; more gathers in flight per CU were
+// measured faster at every step from 3 waves up). The query slices of a wave's 4 rows sit in
+// LDS (16 KiB per workgroup) rather than in registers.
+// LSE: also write the row's base-2 log-sum-exp (the training forward, 4 waves per SIMD).
+// TRUST: the indices are known to lie in [0, T) (they come from this library's retrieval),
+// so the wrap/clamp is skipped.
 // Byte offsets of gathered rows use 24-bit multiplies (T and the row strides below 2^24,
 // checked by the host).
 // VI: lane group g takes the NB consecutive slots g*NB .. g*NB+NB-1 of a task, so its
 // indices arrive in one 16-byte load per task instead of one 4-byte load per step (a quarter
-// of the vector-memory instructions, which all pay the same texture-address cost); needs
+// of the vector-memory instructions); needs
 // K % 4 == 0, 16-byte aligned index rows and K >= NB (checked by the launcher).
 template <typename DT, int D, int NB, bool LSE, bool TRUST, bool VI>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(sizeof(DT) == 2 && !LSE ? 4 : 1)))
@@ -250,36 +251,25 @@ void sparse_readout_fast(ReadoutParams p)
     float* lrow = LSE ? p.lse2 + (b * p.H + h) * p.T + tw : nullptr;   // wave-uniform
     const int64_t irow = p.is[1];
 
-    // stage I: offsets (+ query slice at a row's first task) of the task whose K/V load is next
-    uint32_t ko[NB], vo[NB];
-    uint4 qIlo, qIhi;
-    int ri = 0, qi = 0;   // task of stage I
-    auto fetch_idx = [&]() {
-        const char* ip = reinterpret_cast<const char*>(ib + ri * irow);
-        int jv[NB];
+    // Indices are loaded one pipeline step before the K/V gathers that use them, and issued
+    // ahead of the gathers of the step in between: loads return in issue order, so waiting
+    // for an index load then never waits for K/V rows still in flight.
+    int ri = 0, qi = 0;   // task whose indices load next
+    auto load_idx = [&](int (&jn)[NB]) {   // past the last task: reloads the last row's indices
+        const char* ip = reinterpret_cast<const char*>(ib + min(ri, nrows - 1) * irow);
         if constexpr (VI) {
             // slots past K (masked in the compute) read the row's last NB indices instead
             const int s0 = min(qi * CH + grp * NB, K - NB);
             const uint4 w = *reinterpret_cast<const uint4*>(ip + uint32_t(s0) * 4u);
-            jv[0] = int(w.x); jv[1] = int(w.y); jv[2] = int(w.z); jv[3] = int(w.w);
+            jn[0] = int(w.x); jn[1] = int(w.y); jn[2] = int(w.z); jn[3] = int(w.w);
         } else {
 #pragma unroll
             for (int u = 0; u < NB; ++u) {
                 const int slot = min(qi * CH + u * NPS + grp, K - 1);
-                jv[u] = *reinterpret_cast<const int*>(ip + uint32_t(slot) * 4u);
+                jn[u] = *reinterpret_cast<const int*>(ip + uint32_t(slot) * 4u);
             }
         }
-#pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            int j = jv[u];
-            if constexpr (!TRUST) {
-                j += (j >> 31) & T;
-                j = min(max(j, 0), T - 1);
-            }
-            ko[u] = __umul24(uint32_t(j), krow) + loff;
-            vo[u] = __umul24(uint32_t(j), vrow) + loff;
-        }
-        if (qi == 0) ld16<DT>(qb, uint32_t(ri) * qrow + loff, qIlo, qIhi);
+        if (++qi == nb) { qi = 0; ++ri; }
     };
     auto advance = [&](int& r, int& q) { if (++q == nb) { q = 0; ++r; } };
 
@@ -289,11 +279,23 @@ void sparse_readout_fast(ReadoutParams p)
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int rc = 0, qc = 0;   // task being computed
 
+    // the query slices of the wave's rows, loaded once ahead of the pipeline and parked in
+    // LDS (otherwise unused here) rather than in registers
+    constexpr int QW = sizeof(DT) == 4 ? 2 : 1;   // 16-byte words per lane and row
+    __shared__ uint4 sq[kWaves][kRowsPerWave][QW][64];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        uint4 lo, hi;
+        ld16<DT>(qb, uint32_t(min(r, nrows - 1)) * qrow + loff, lo, hi);
+        sq[wave][r][0][lane] = lo;
+        if constexpr (QW == 2) sq[wave][r][QW - 1][lane] = hi;
+    }
+
     auto compute = [&](const uint4 (&klo)[NB], const uint4 (&khi)[NB], const uint4 (&vlo)[NB],
-                       const uint4 (&vhi)[NB], const uint4& qnlo, const uint4& qnhi) {
-        if (qc == 0) {
-            qlo = qnlo;
-            qhi = qnhi;
+                       const uint4 (&vhi)[NB]) {
+        if (qc == 0) {   // the wave's own LDS slot: no barrier needed
+            qlo = sq[wave][rc][0][lane];
+            if constexpr (QW == 2) qhi = sq[wave][rc][QW - 1][lane];
             m = -__builtin_inff();
             l = 0.0f;
 #pragma unroll
@@ -355,33 +357,36 @@ void sparse_readout_fast(ReadoutParams p)
     };
 
     const int ntask = nrows * nb;
-    uint4 qAlo, qAhi, qBlo, qBhi;
     uint4 kAlo[NB], kAhi[NB], vAlo[NB], vAhi[NB], kBlo[NB], kBhi[NB], vBlo[NB], vBhi[NB];
-    fetch_idx();
+    int jA[NB], jB[NB];
+    auto gather = [&](const int (&jn)[NB], uint4 (&klo)[NB], uint4 (&khi)[NB], uint4 (&vlo)[NB],
+                      uint4 (&vhi)[NB]) {
 #pragma unroll
-    for (int u = 0; u < NB; ++u) { ld16<DT>(kb, ko[u], kAlo[u], kAhi[u]); ld16<DT>(vb, vo[u], vAlo[u], vAhi[u]); }
-    qAlo = qIlo; qAhi = qIhi;
-    advance(ri, qi);
-    if (ntask > 1) fetch_idx();
-    for (int tau = 0; tau < ntask; tau += 2) {
-        if (tau + 1 < ntask) {
-#pragma unroll
-            for (int u = 0; u < NB; ++u) { ld16<DT>(kb, ko[u], kBlo[u], kBhi[u]); ld16<DT>(vb, vo[u], vBlo[u], vBhi[u]); }
-            qBlo = qIlo; qBhi = qIhi;
-            advance(ri, qi);
-            if (tau + 2 < ntask) fetch_idx();
-        }
-        compute(kAlo, kAhi, vAlo, vAhi, qAlo, qAhi);
-        if (tau + 1 < ntask) {
-            if (tau + 2 < ntask) {
-#pragma unroll
-                for (int u = 0; u < NB; ++u) { ld16<DT>(kb, ko[u], kAlo[u], kAhi[u]); ld16<DT>(vb, vo[u], vAlo[u], vAhi[u]); }
-                qAlo = qIlo; qAhi = qIhi;
-                advance(ri, qi);
-                if (tau + 3 < ntask) fetch_idx();
+        for (int u = 0; u < NB; ++u) {
+            int j = jn[u];
+            if constexpr (!TRUST) {
+                j += (j >> 31) & T;
+                j = min(max(j, 0), T - 1);
             }
-            compute(kBlo, kBhi, vBlo, vBhi, qBlo, qBhi);
+            ld16<DT>(kb, __umul24(uint32_t(j), krow) + loff, klo[u], khi[u]);
+            ld16<DT>(vb, __umul24(uint32_t(j), vrow) + loff, vlo[u], vhi[u]);
         }
+    };
+    // per step: indices of task tau+2, K/V of task tau+1, compute task tau. Every load is
+    // issued unconditionally (tasks past the end reload the last row's indices, in bounds,
+    // unused): a load under a condition would leave the wait counts unknown and the compiler
+    // would wait for every load in flight; as it is, each wait is for loads issued before the
+    // gathers still in flight.
+    load_idx(jA);
+    gather(jA, kAlo, kAhi, vAlo, vAhi);
+    load_idx(jB);
+    for (int tau = 0; tau < ntask; tau += 2) {
+        load_idx(jA);
+        gather(jB, kBlo, kBhi, vBlo, vBhi);
+        compute(kAlo, kAhi, vAlo, vAhi);
+        load_idx(jB);
+        gather(jA, kAlo, kAhi, vAlo, vAhi);
+        if (tau + 1 < ntask) compute(kBlo, kBhi, vBlo, vBhi);
     }
 }
 
