@@ -44,7 +44,10 @@ constexpr int kWaves = WF_TOPK_WAVES;                  // waves per workgroup (s
 constexpr int kBins = 128;                             // pruning histogram bins per row
 constexpr int kPD = 4;                                 // key steps each wave keeps in flight
 constexpr int kUnitMax = 2 * 16 * kWaves;              // appends per row in one 2-step unit, at most
-constexpr float kEpsRel = 1.0f / 4096.0f;              // 2^-12: > 20x the MFMA/FMA error bound
+// |MFMA score - exact score| <= 2 * n * 2^-24 * sum_d |q_d k_d| for n accumulated terms with
+// round-to-nearest in both (2^-23 per term with truncating adds); the bound used is 2^-20
+// per term: 8x the round-to-nearest bound, 4x the truncating one
+constexpr float kEpsPerTerm = 1.0f / 1048576.0f;
 constexpr float kTiny = 7.888609052210118e-31f;        // 2^-100: covers denormal flushing
 
 // ------------------------------------------------------------------ operand loads
@@ -683,7 +686,7 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
     if (threadIdx.x < kRows) {
         float l1 = 0.0f;
         for (int d = 0; d < RP; ++d) l1 += fabsf(sm.q[threadIdx.x][d]);
-        sm.eps[threadIdx.x] = kEpsRel * (l1 * 1.0001f) * (mk + kTiny) + kTiny;
+        sm.eps[threadIdx.x] = kEpsPerTerm * float(RP) * (l1 * 1.0001f) * (mk + kTiny) + kTiny;
     }
     __syncthreads();
 
