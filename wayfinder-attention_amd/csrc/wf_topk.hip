@@ -206,6 +206,14 @@ __device__ __forceinline__ int row_max16_i32(int x)
     x = max(x, int(dpp32<kRor1>(uint32_t(x))));
     return x;
 }
+__device__ __forceinline__ int row_sum16_i32(int x)
+{
+    x += int(dpp32<kRor8>(uint32_t(x)));
+    x += int(dpp32<kRor4>(uint32_t(x)));
+    x += int(dpp32<kRor2>(uint32_t(x)));
+    x += int(dpp32<kRor1>(uint32_t(x)));
+    return x;
+}
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp64(uint64_t x)
 {
@@ -364,7 +372,30 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
     int b, gt, eq;
     find_boundary(hist, u, K, b, gt, eq);
     // one bin of slack absorbs the rounding of the bin computation
-    const float theta = b >= 1 ? lo + float(b - 1) * (span / float(kBins)) : lo;
+    float theta = b >= 1 ? lo + float(b - 1) * (span / float(kBins)) : lo;
+    int keep_lin = 0;
+#pragma unroll
+    for (int m = 0; m < EPR; ++m) keep_lin += s[m] >= theta - 2.0f * eps ? 1 : 0;
+    keep_lin = row_sum16_i32(keep_lin);
+    if (keep_lin > K + K / 4) {
+        // the cut would keep too much: heavy-tailed scores, whose few large values stretch
+        // [lo, hi] and crowd the rest into the lowest bins. Second histogram in the
+        // order-preserving integer image of the scores (2^sh consecutive images per bin:
+        // relative resolution); integer arithmetic makes its bin edges exact, so an entry in
+        // bin >= b2 has score >= theta2
+        const uint32_t olo = ord_f32(lo), ohi = ord_f32(hi);
+        const int sh = max(0, 32 - __clz(int(ohi - olo)) - 7);
+        reinterpret_cast<uint4*>(hist)[2 * u] = make_uint4(0, 0, 0, 0);
+        reinterpret_cast<uint4*>(hist)[2 * u + 1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int m = 0; m < EPR; ++m) {
+            const uint32_t bin = (ord_f32(s[m]) - olo) >> sh;
+            atomicAdd(&hist[s[m] >= lo ? bin : uint32_t(kBins + u)], 1u);
+        }
+        int b2, gt2, eq2;
+        find_boundary(hist, u, K, b2, gt2, eq2);
+        theta = fmaxf(theta, unord_f32(olo + (uint32_t(b2) << sh)));
+    }
     const float kappa = theta - 2.0f * eps;
     // compaction: each lane's survivors go, in order, after those of the higher lanes of the
     // row (all entries are in registers, so the in-place writes cannot clobber unread ones);
