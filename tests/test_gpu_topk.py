@@ -135,6 +135,16 @@ def test_topk_config5_heavy_tail_sampled(device):
     _check_exact(qa, ka, 256, device, rows=rows)
 
 
+@pytest.mark.parametrize("K,dtype", [(256, torch.bfloat16), (100, torch.float32), (64, torch.float16)])
+def test_topk_heavy_tail_full(device, K, dtype):
+    """Student-t(3) addresses on every row: a few large keys stretch each pool's score range,
+    which sends the pruning to its second, order-preserving histogram (and the exact fallback
+    when scores crowd); indices and scores must still equal the oracle's."""
+    _say(f"[topk] heavy tail full T=6000 K={K} {dtype}")
+    qa, ka = addresses(2, 6000, 32, seed=4000 + K, dtype=torch.float32, dist="student_t")
+    _check_exact(qa.to(dtype), ka.to(dtype), K, device)
+
+
 def test_topk_deterministic(device):
     _say("[topk] determinism")
     qa, ka = addresses(2, 3000, 32, seed=77, dtype=torch.bfloat16)
