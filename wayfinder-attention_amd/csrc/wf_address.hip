@@ -17,7 +17,8 @@
 namespace wf {
 namespace {
 
-constexpr int kTok = 64;          // tokens per workgroup
+constexpr int kTPT = 2;           // tokens per thread
+constexpr int kTok = 16 * kTPT;   // tokens per workgroup (512 workgroups at 16384 tokens)
 constexpr int kOut = 64;          // output rows per workgroup: q in rows 0..31, k in 32..63
 constexpr int kChunk = 256;       // d_model columns staged per LDS round
 constexpr int kPitch = kChunk + 8;  // LDS row pitch in elements (16 B pad: conflict-free rows)
@@ -76,7 +77,7 @@ __device__ __forceinline__ float dot_chunk(const uint4& a, const uint4& b)
     }
 }
 
-// Thread layout: tb = tid / 16 picks tokens 4tb..4tb+3, ob = tid % 16 picks output rows
+// Thread layout: tb = tid / 16 picks tokens kTPT*tb.., ob = tid % 16 picks output rows
 // 4ob..4ob+3; lanes 0-7 of each 16-lane group hold q rows, lanes 8-15 k rows, so one
 // 8-lane shuffle reduction gives a token's squared norm.
 template <typename DT>
@@ -91,40 +92,67 @@ __global__ __launch_bounds__(256) void address_project_kernel(AddressParams p)
     const int64_t tok0 = int64_t(blockIdx.x) * kTok;
     const int D = int(p.d_model);
     const DT* x = static_cast<const DT*>(p.x);
-    float acc[4][4] = {};
+    float acc[kTPT][4] = {};
 
+    // staging: every thread issues all of its 16-byte loads of a round (token tile, then the
+    // weight tile) before the first LDS store, so a round waits on memory once
+    constexpr int NCH = kChunk / EPC;                     // 16-byte chunks per full row
+    constexpr int kXPer = kTok * NCH / 256;              // loads per thread and tile
+    constexpr int kWPer = kOut * NCH / 256;
+    // element offset of each token row of the tile (one 64-bit division per row, by kTok
+    // threads, instead of one per load)
+    __shared__ int64_t row_off[kTok];
+    __shared__ int64_t row_b[kTok], row_t[kTok];
+    if (tid < kTok) {
+        const int64_t n = min(tok0 + tid, p.n_tokens - 1);
+        const int64_t b = n / p.T, t = n % p.T;
+        row_off[tid] = b * p.xs[0] + t * p.xs[1];
+        row_b[tid] = b;
+        row_t[tid] = t;
+    }
+    __syncthreads();
     for (int c0 = 0; c0 < D; c0 += kChunk) {
         const int cw = min(kChunk, D - c0);       // multiple of 8 (checked by the entry point)
         const int nch = cw / EPC;                 // 16-byte chunks per row in this round
-        __syncthreads();
-        for (int i = tid; i < kTok * nch; i += 256) {
-            const int r = i / nch, c = i % nch;
-            const int64_t n = tok0 + r;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (n < p.n_tokens) {
-                const int64_t b = n / p.T, t = n % p.T;
-                v = *reinterpret_cast<const uint4*>(x + b * p.xs[0] + t * p.xs[1] + c0 + c * EPC);
-            }
-            *reinterpret_cast<uint4*>(&xs[r * kPitch + c * EPC]) = v;
+        uint4 xv[kXPer], wv[kWPer];
+#pragma unroll
+        for (int k = 0; k < kXPer; ++k) {
+            const int i = tid + 256 * k;
+            const int r = i / NCH, c = i % NCH;   // compile-time divisor
+            xv[k] = make_uint4(0, 0, 0, 0);
+            if (c < nch && tok0 + r < p.n_tokens)
+                xv[k] = *reinterpret_cast<const uint4*>(x + row_off[r & (kTok - 1)] + c0 + c * EPC);
         }
-        for (int i = tid; i < kOut * nch; i += 256) {
-            const int r = i / nch, c = i % nch;
+#pragma unroll
+        for (int k = 0; k < kWPer; ++k) {
+            const int i = tid + 256 * k;
+            const int r = i / NCH, c = i % NCH;
             const int half = r / 32, o = r % 32;
-            uint4 v = make_uint4(0, 0, 0, 0);
             const DT* w = half == 0 ? static_cast<const DT*>(p.wq) : static_cast<const DT*>(p.wk);
-            if (o < p.R && w != nullptr) v = *reinterpret_cast<const uint4*>(w + int64_t(o) * p.w_stride + c0 + c * EPC);
-            *reinterpret_cast<uint4*>(&ws[r * kPitch + c * EPC]) = v;
+            wv[k] = make_uint4(0, 0, 0, 0);
+            if (c < nch && o < p.R && w != nullptr)
+                wv[k] = *reinterpret_cast<const uint4*>(w + int64_t(o) * p.w_stride + c0 + c * EPC);
+        }
+        __syncthreads();   // the previous round's tiles are consumed
+#pragma unroll
+        for (int k = 0; k < kXPer; ++k) {
+            const int i = tid + 256 * k;
+            if (i % NCH < nch) *reinterpret_cast<uint4*>(&xs[(i / NCH) * kPitch + (i % NCH) * EPC]) = xv[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kWPer; ++k) {
+            const int i = tid + 256 * k;
+            if (i % NCH < nch) *reinterpret_cast<uint4*>(&ws[(i / NCH) * kPitch + (i % NCH) * EPC]) = wv[k];
         }
         __syncthreads();
         for (int c = 0; c < nch; ++c) {
-            uint4 xv[4], wv[4];
+            uint4 xv[kTPT], wv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xv[i] = *reinterpret_cast<const uint4*>(&xs[(tb * 4 + i) * kPitch + c * EPC]);
-                wv[i] = *reinterpret_cast<const uint4*>(&ws[(ob * 4 + i) * kPitch + c * EPC]);
-            }
+            for (int i = 0; i < kTPT; ++i) xv[i] = *reinterpret_cast<const uint4*>(&xs[(tb * kTPT + i) * kPitch + c * EPC]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const uint4*>(&ws[(ob * 4 + i) * kPitch + c * EPC]);
+#pragma unroll
+            for (int i = 0; i < kTPT; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] += dot_chunk<DT>(xv[i], wv[j]);
         }
@@ -146,7 +174,7 @@ __global__ __launch_bounds__(256) void address_project_kernel(AddressParams p)
     DT* out = static_cast<DT*>(half == 0 ? p.out_q : p.out_k);
     const int64_t* os = half == 0 ? p.oqs : p.oks;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kTPT; ++i) {
         float y[4], ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -155,10 +183,9 @@ __global__ __launch_bounds__(256) void address_project_kernel(AddressParams p)
         }
         ss = sum8(ss);
         const float den = fmaxf(round_to<DT>(sqrtf(ss)), 1e-12f);   // norm(...).clamp_min(eps)
-        const int64_t n = tok0 + tb * 4 + i;
+        const int64_t n = tok0 + tb * kTPT + i;
         if (n < p.n_tokens && out != nullptr) {
-            const int64_t b = n / p.T, t = n % p.T;
-            DT* orow = out + b * os[0] + t * os[1];
+            DT* orow = out + row_b[tb * kTPT + i] * os[0] + row_t[tb * kTPT + i] * os[1];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 if (o0 + j < p.R) {
