@@ -38,6 +38,8 @@ CONFIGS = {
     "c5": (1, 8, 65536, 128, 32, 256, torch.bfloat16, "student_t"),
 }
 HBM_PEAK_GBS = 8000.0
+# dense MFMA peaks of one MI355X (TFLOP/s) for the retrieval's score tiles, by input dtype
+MFMA_PEAK_TFLOPS = {torch.bfloat16: 2500.0, torch.float16: 2500.0, torch.float32: 157.3}
 
 
 def algorithmic_bytes(B, H, T, D, R, K, s):
@@ -314,6 +316,7 @@ def main():
     ms_read = time_loop(lambda: sparse_meat_attention(dev["q"], dev["k"], dev["v"], idx, scale),
                         args.steps, 3)
     read_gbs = readout_bytes / (ms_read * 1e-3) / 1e9
+    score_flops = B * R * T * (T + 1)
 
     dense = None
     if not args.no_dense:
@@ -352,13 +355,19 @@ def main():
                        "p90": round(p90, 4)},
         "rows_per_s": round(B * T / (ms * 1e-3), 1),
         "kernels_ms": {"causal_topk": round(ms_topk, 4), "sparse_readout": round(ms_read, 4)},
-        "roofline": {"bound": "hbm", "kernel": "sparse_readout_kernel",
+        "roofline": {"bound": "hbm", "kernel": "sparse_readout_fast",
                      "achieved": round(read_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(read_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": readout_bytes},
         "path_roofline": {"algorithmic_bytes": path_bytes,
                           "achieved_gbs": round(path_bytes / (ms * 1e-3) / 1e9, 1),
                           "frac": round(path_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        # the retrieval's score contraction (q_addr . k_addr over the causal triangle,
+        # B*d_A*T*(T+1) flops) against the dense MFMA peak: it is far from that bound
+        "retrieval_mfma": {"kernel": "causal_topk_kernel", "flops": score_flops,
+                           "achieved": round(score_flops / (ms_topk * 1e-3) / 1e12, 2),
+                           "peak": MFMA_PEAK_TFLOPS[dtype], "unit": "TFLOP/s",
+                           "frac": round(score_flops / (ms_topk * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS[dtype], 5)},
         "peak_mb": round(peak_mb, 1),
         "dense_causal_sdpa": dense,
         "vs_dense": round(dense["median_ms"] / med, 3) if dense else None,

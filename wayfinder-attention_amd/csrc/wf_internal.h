@@ -187,6 +187,10 @@ constexpr int kReadoutRowsPerWG = 16;
 // fast kernel's 5 waves per SIMD): grids above this run in several residency waves.
 constexpr int64_t kReadoutResidentWGs = 1280;
 
+// Retrieval workgroups that fill one slot of every CU on MI355X (256 CUs, two retrieval
+// workgroups per CU): in the first residency wave workgroups c and c + 256 share a CU.
+constexpr int64_t kTopkCUs = 256;
+
 // launchers (return hipError_t of the launch)
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s);
