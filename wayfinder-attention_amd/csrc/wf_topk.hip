@@ -43,7 +43,7 @@ constexpr int kRows = 16;                              // query rows per workgro
 constexpr int kWaves = WF_TOPK_WAVES;                  // waves per workgroup (split the keys)
 constexpr int kBins = 128;                             // pruning histogram bins per row
 constexpr int kPD = 4;                                 // key steps each wave keeps in flight
-constexpr int kUnitMax = 2 * 16 * kWaves;              // appends per row in one 2-step unit, at most
+constexpr int kStepMax = 16 * kWaves;                  // appends per row in one key step of every wave, at most
 // |MFMA score - exact score| <= 2 * n * 2^-24 * sum_d |q_d k_d| for n accumulated terms with
 // round-to-nearest in both (2^-23 per term with truncating adds); the bound used is 2^-20
 // per term: 8x the round-to-nearest bound, 4x the truncating one
@@ -664,7 +664,12 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
     // pool entries per row: two workgroups (<= 80 KiB of LDS each) per CU for RC <= 2; the
     // wide variant runs one workgroup per CU (register-bound) and has LDS to spare
     constexpr int POOL = 512;
-    constexpr int LIMIT = POOL - kUnitMax;       // a pool above this is pruned at the next check
+    // pool checks every CG key steps: every step for K > 128, whose pruned pools keep so many
+    // entries that the room a check interval must reserve decides how often they are pruned
+    // (config 5: 18.5 -> 11.3 prunes per block, 2.20 -> 2.04 ms), every 2 steps otherwise
+    // (fewer barriers; config 4 is 1-2 % faster that way)
+    constexpr int CG = KP2 >= 256 ? 1 : 2;
+    constexpr int LIMIT = POOL - CG * kStepMax;  // a pool above this is pruned at the next check
     constexpr int HEADROOM = 64;                 // a prune must leave this much room
     static_assert(LIMIT - HEADROOM > KP2 + 32, "pool too small for K");
     static_assert(sizeof(TopkSmem<RP, POOL>) <= (RC <= 2 ? 80 : 160) * 1024, "LDS per workgroup");
@@ -786,11 +791,12 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
         for (int c = 0; c < RC; ++c) acc = mfma_chunk<DT>(alo[c], ahi[c], qlo[c], qhi[c], acc);
         return acc;
     };
-    // budget: 2-step units every wave may still take before a pool could overflow (a unit
-    // appends at most kUnitMax per row). Every wave must take the same decisions at a check
-    // (the barriers must pair up), so they all decide on one snapshot of the counts: a second
-    // barrier keeps every wave from appending again until all of them have read it.
-    int budget = max(1, (POOL - 0) / kUnitMax);
+    // budget: check intervals (CG key steps) every wave may still take before a pool could
+    // overflow (a step of all waves appends at most kStepMax per row). Every wave must take
+    // the same decisions at a check (the barriers must pair up), so they all decide on one
+    // snapshot of the counts: a second barrier keeps every wave from appending again until
+    // all of them have read it.
+    int budget = max(1, (POOL - 0) / (CG * kStepMax));
     auto check = [&]() {
         __syncthreads();   // every append of the unit has landed
         int cl = lane < kRows ? sm.cnt[lane] : 0;
@@ -819,7 +825,7 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
 #endif
         }
         const int cmax = __builtin_amdgcn_readfirstlane(row_max16_i32(cl));
-        budget = max(1, (POOL - cmax) / kUnitMax);
+        budget = max(1, (POOL - cmax) / (CG * kStepMax));
     };
     if (iters > 0) {
         uint4 blo[kPD][RC], bhi[kPD][RC];
@@ -841,6 +847,9 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
                 load_step(16 * min(st0 + kWaves * kPD, nfull - 1), blo[h], bhi[h]);
                 load_step(16 * min(st1 + kWaves * kPD, nfull - 1), blo[h + 1], bhi[h + 1]);
                 if (st0 < nfull) consider(acc0, st0 * 16 + 4 * g);
+                if constexpr (CG == 1) {
+                    if (--budget == 0) check();
+                }
                 if (st1 < nfull) consider(acc1, st1 * 16 + 4 * g);
                 if (--budget == 0) check();
             }
