@@ -612,6 +612,16 @@ __device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
     }
     int32_t* oi = out_idx + row * k_eff;
     float* os = out_scores ? out_scores + row * k_eff : nullptr;
+    if (kept == KP2 && k_eff == KP2 && !os && (reinterpret_cast<uintptr_t>(oi) & 15u) == 0) {
+        // a full row without scores: each lane's EPL consecutive slots leave as 16-byte stores
+        uint32_t v[EPL];
+#pragma unroll
+        for (int m = 0; m < EPL; ++m) v[m] = 0xffffffffu - uint32_t(key[m]);
+        uint4* o4 = reinterpret_cast<uint4*>(oi + u * EPL);
+#pragma unroll
+        for (int m = 0; m < EPL / 4; ++m) o4[m] = make_uint4(v[4 * m], v[4 * m + 1], v[4 * m + 2], v[4 * m + 3]);
+        return;
+    }
 #pragma unroll
     for (int m = 0; m < EPL; ++m) {
         const int64_t i = u * EPL + m;
