@@ -335,12 +335,12 @@ __device__ __forceinline__ Entry key_entry(uint64_t k)
 // Histogram pruning of a row whose pool holds c > K entries. Returns false when the scores
 // are too close together to separate (the caller then rescores exactly); otherwise the
 // pool is cut to the entries >= theta' - 2 eps, c_out is the new count (uniform over the
-// row's lanes) and, from lane u == 0, cnt / thr are stored for the other waves.
-template <int POOL>
+// row's lanes) and, from lane u == 0, cnt / thr are stored for the other waves. Each lane
+// reads EPR slots (c <= 16 EPR).
+template <int EPR, int POOL>
 __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& cnt,
                           float& thr, float eps, int K, int u)
 {
-    constexpr int EPR = POOL / 16;
     c_out = c;
     // every slot is read unconditionally (slots >= c hold stale data and are masked below), so
     // the reads issue back to back and the row waits on LDS once
@@ -414,6 +414,31 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
     c_out = total;
     if (u == 0) { cnt = total; thr = kappa; }
     return true;
+}
+
+// prune_row sized to the fullest pool among the wave's four rows (cw, wave-uniform, so the
+// wave takes one branch): a final prune sees ~220 entries and an in-loop one ~400, and
+// every slot read costs the histogram, count and compaction work of an entry (config 4:
+// final prune 3.6 -> 2.7 us per block). SIZED = false reads the whole pool: the K = 256
+// kernels, where the extra variants push the register allocator into scratch spills
+// (88 bytes per lane, config 5 1.5x slower).
+template <bool SIZED, int POOL>
+__device__ bool prune_sized(Entry* pool, uint32_t* hist, int c, int cw, int& c_out, int& cnt,
+                            float& thr, float eps, int K, int u)
+{
+    if constexpr (SIZED) {
+        if (POOL / 16 > 16 && cw <= 16 * 16) return prune_row<16, POOL>(pool, hist, c, c_out, cnt, thr, eps, K, u);
+        if (POOL / 16 > 24 && cw <= 16 * 24) return prune_row<24, POOL>(pool, hist, c, c_out, cnt, thr, eps, K, u);
+    }
+    return prune_row<POOL / 16, POOL>(pool, hist, c, c_out, cnt, thr, eps, K, u);
+}
+
+// largest value of v over the wave's four 16-lane rows (v uniform within each row)
+__device__ __forceinline__ int wave_max_of_rows(int v)
+{
+    const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return max(max(a, b), max(c, d));
 }
 
 // Exact rescoring of a row's c pool entries: pool[e].s becomes the exact score. The VEC
@@ -816,10 +841,11 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
             const uint64_t tc0 = wall_clock64();
 #endif
             const int c = rr < kRows ? sm.cnt[rr] : 0;
+            const int cw = wave_max_of_rows(c);
             if (c > K) {
                 int c2 = c;
-                const bool ok = prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr],
-                                                sm.thr[rr], sm.eps[rr], K, u);
+                const bool ok = prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr],
+                                                  sm.thr[rr], sm.eps[rr], K, u);
                 if (!ok || c2 > LIMIT - HEADROOM)
                     exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c2, sm.cnt[rr],
                                                  sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
@@ -895,14 +921,16 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
     uint64_t tmA = 0, tmB = 0;
     int c_in = 0, c_pr = 0;
 #endif
-    if (rr < kRows && r0 + rr < T) {
+    const bool row_live = rr < kRows && r0 + rr < T;
+    const int cw = wave_max_of_rows(row_live ? sm.cnt[rr] : 0);
+    if (row_live) {
         int c = sm.cnt[rr];
 #ifdef WF_TOPK_TIMING
         c_in = c;
 #endif
         if (c > K) {
             int c2 = c;
-            prune_row<POOL>(sm.pool[rr], sm.hist[rr], c, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
+            prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
             c = c2;
         }
 #ifdef WF_TOPK_TIMING
