@@ -574,14 +574,20 @@ __device__ int select_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& t
 // Exact rescoring of a row's c pool entries and exact selection of its min(K, c) best by
 // (score desc, index asc); the winners end up in pool[0..kept) with exact scores. Returns
 // kept (uniform over the row); lane u == 0 stores cnt and the exact threshold s_K - eps.
-template <typename DT, bool VEC, int RP, int POOL>
-__device__ int exact_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& thr,
+// The selection reads ceil(cw / 16) entries per lane, cw >= c being the fullest pool among
+// the wave's rows (wave-uniform, so the wave takes one branch): after a final prune a
+// K = 128 pool holds ~135 entries. SIZED adds the 9-entry variant (K <= 128 kernels; the
+// K = 256 ones stay within their register budget without it).
+template <typename DT, bool VEC, int RP, int POOL, bool SIZED>
+__device__ int exact_row(Entry* pool, uint32_t* hist, int c, int cw, int& cnt, float& thr,
                          float eps, const float* q, const DT* kb, int64_t kst, int64_t ksr, int R,
                          int K, int u)
 {
     rescore_row<DT, VEC, RP>(pool, c, q, kb, kst, ksr, R, u);
-    constexpr int kSmall = 12;   // after a prune the pool rarely holds more than K + 64
-    if (c <= 16 * kSmall) return select_row<kSmall>(pool, hist, c, cnt, thr, eps, K, u);
+    if constexpr (SIZED) {
+        if (cw <= 16 * 9) return select_row<9>(pool, hist, c, cnt, thr, eps, K, u);
+    }
+    if (cw <= 16 * 12) return select_row<12>(pool, hist, c, cnt, thr, eps, K, u);
     return select_row<POOL / 16>(pool, hist, c, cnt, thr, eps, K, u);
 }
 
@@ -847,7 +853,7 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
                 const bool ok = prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr],
                                                   sm.thr[rr], sm.eps[rr], K, u);
                 if (!ok || c2 > LIMIT - HEADROOM)
-                    exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c2, sm.cnt[rr],
+                    exact_row<DT, VEC, RP, POOL, false>(sm.pool[rr], sm.hist[rr], c2, POOL, sm.cnt[rr],
                                                  sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
                                                  p.ksr, R, K, u);
             }
@@ -922,24 +928,25 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
     int c_in = 0, c_pr = 0;
 #endif
     const bool row_live = rr < kRows && r0 + rr < T;
-    const int cw = wave_max_of_rows(row_live ? sm.cnt[rr] : 0);
+    int c = row_live ? sm.cnt[rr] : 0;   // rows past T hold 0 in every lane
+#ifdef WF_TOPK_TIMING
+    c_in = c;
+#endif
+    const int cw = wave_max_of_rows(c);
+    if (row_live && c > K) {
+        int c2 = c;
+        prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
+        c = c2;
+    }
+#ifdef WF_TOPK_TIMING
+    tmA = wall_clock64();
+    c_pr = c;
+#endif
+    const int cw2 = wave_max_of_rows(c);   // counts after the prune, every lane of the wave
     if (row_live) {
-        int c = sm.cnt[rr];
-#ifdef WF_TOPK_TIMING
-        c_in = c;
-#endif
-        if (c > K) {
-            int c2 = c;
-            prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
-            c = c2;
-        }
-#ifdef WF_TOPK_TIMING
-        tmA = wall_clock64();
-        c_pr = c;
-#endif
-        const int kept = exact_row<DT, VEC, RP, POOL>(sm.pool[rr], sm.hist[rr], c, sm.cnt[rr],
-                                                      sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
-                                                      p.ksr, R, K, u);
+        const int kept = exact_row<DT, VEC, RP, POOL, (KP2 <= 128)>(sm.pool[rr], sm.hist[rr], c, cw2,
+                                                                   sm.cnt[rr], sm.thr[rr], sm.eps[rr],
+                                                                   sm.q[rr], kb, p.kst, p.ksr, R, K, u);
 #ifdef WF_TOPK_TIMING
         tmB = wall_clock64();
         emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, p.out_idx + b * T * p.k_eff,
