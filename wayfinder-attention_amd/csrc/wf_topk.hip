@@ -417,7 +417,7 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
 }
 
 // prune_row sized to the fullest pool among the wave's four rows (cw, wave-uniform, so the
-// wave takes one branch): a final prune sees ~220 entries and an in-loop one ~400, and
+// wave takes one branch): a final prune sees ~220 entries and an in-loop one 385-450, and
 // every slot read costs the histogram, count and compaction work of an entry (config 4:
 // final prune 3.6 -> 2.7 us per block). SIZED = false reads the whole pool: the K = 256
 // kernels, where the extra variants push the register allocator into scratch spills
@@ -429,6 +429,7 @@ __device__ bool prune_sized(Entry* pool, uint32_t* hist, int c, int cw, int& c_o
     if constexpr (SIZED) {
         if (POOL / 16 > 16 && cw <= 16 * 16) return prune_row<16, POOL>(pool, hist, c, c_out, cnt, thr, eps, K, u);
         if (POOL / 16 > 24 && cw <= 16 * 24) return prune_row<24, POOL>(pool, hist, c, c_out, cnt, thr, eps, K, u);
+        if (POOL / 16 > 28 && cw <= 16 * 28) return prune_row<28, POOL>(pool, hist, c, c_out, cnt, thr, eps, K, u);
     }
     return prune_row<POOL / 16, POOL>(pool, hist, c, c_out, cnt, thr, eps, K, u);
 }
