@@ -814,13 +814,17 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
     };
     // append the lane's candidates (keys jb .. jb+3 of row n) that reach the threshold; one
     // LDS atomic reserves their slots, the others are written to a dummy slot of the row
+    // the row's pool and this lane's dummy slot as LDS pointers, formed once: an append then
+    // advances one pointer instead of recomputing a slot address per entry
+    Entry* const pool_row = sm.pool[n];
+    Entry* const pool_dummy = pool_row + POOL + g;
     auto append = [&](const f32x4_t& acc, const bool (&pp)[4], int jb) {
         const int cntp = int(pp[0]) + int(pp[1]) + int(pp[2]) + int(pp[3]);
-        int pos = atomicAdd(&sm.cnt[n], cntp);
+        Entry* dst = pool_row + atomicAdd(&sm.cnt[n], cntp);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            sm.pool[n][pp[i] ? pos : POOL + g] = Entry{acc[i], uint32_t(jb + i)};
-            pos += int(pp[i]);
+            *(pp[i] ? dst : pool_dummy) = Entry{acc[i], uint32_t(jb + i)};
+            dst += int(pp[i]);
         }
     };
     auto consider = [&](const f32x4_t& acc, int jb) {
