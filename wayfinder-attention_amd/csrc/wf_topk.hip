@@ -353,8 +353,8 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
 #pragma unroll
     for (int m = 0; m < EPR; ++m) {
         s[m] = u + 16 * m < c ? __uint_as_float(ent[m].x) : __builtin_nanf("");
-        lo = s[m] < lo ? s[m] : lo;
-        hi = s[m] > hi ? s[m] : hi;
+        lo = fminf(lo, s[m]);   // minNum / maxNum: NaN entries leave the bound unchanged
+        hi = fmaxf(hi, s[m]);
     }
     lo = row_min16(lo);
     hi = row_max16(hi);
@@ -373,10 +373,11 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
     find_boundary(hist, u, K, b, gt, eq);
     // one bin of slack absorbs the rounding of the bin computation
     float theta = b >= 1 ? lo + float(b - 1) * (span / float(kBins)) : lo;
-    int keep_lin = 0;
+    int keep_lane = 0;   // this lane's survivors of the linear cut, reused by the compaction
 #pragma unroll
-    for (int m = 0; m < EPR; ++m) keep_lin += s[m] >= theta - 2.0f * eps ? 1 : 0;
-    keep_lin = row_sum16_i32(keep_lin);
+    for (int m = 0; m < EPR; ++m) keep_lane += s[m] >= theta - 2.0f * eps ? 1 : 0;
+    const int keep_lin = row_sum16_i32(keep_lane);
+    bool raised = false;   // uniform over the row
     if (keep_lin > K + K / 4) {
         // the cut would keep too much: heavy-tailed scores, whose few large values stretch
         // [lo, hi] and crowd the rest into the lowest bins. Second histogram in the
@@ -394,15 +395,22 @@ __device__ bool prune_row(Entry* pool, uint32_t* hist, int c, int& c_out, int& c
         }
         int b2, gt2, eq2;
         find_boundary(hist, u, K, b2, gt2, eq2);
-        theta = fmaxf(theta, unord_f32(olo + (uint32_t(b2) << sh)));
+        const float theta2 = unord_f32(olo + (uint32_t(b2) << sh));
+        if (theta2 > theta) {
+            theta = theta2;
+            raised = true;
+        }
     }
     const float kappa = theta - 2.0f * eps;
     // compaction: each lane's survivors go, in order, after those of the higher lanes of the
     // row (all entries are in registers, so the in-place writes cannot clobber unread ones);
     // dropped entries are written to the lane's dummy slot
-    int mine = 0;
+    int mine = keep_lane;
+    if (raised) {
+        mine = 0;
 #pragma unroll
-    for (int m = 0; m < EPR; ++m) mine += s[m] >= kappa ? 1 : 0;
+        for (int m = 0; m < EPR; ++m) mine += s[m] >= kappa ? 1 : 0;
+    }
     int pos = row_suffix_excl16(mine);
     const int total = row_max16_i32(pos + mine);
 #pragma unroll
