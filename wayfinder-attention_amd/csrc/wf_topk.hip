@@ -600,6 +600,66 @@ __device__ int exact_row(Entry* pool, uint32_t* hist, int c, int cw, int& cnt, f
     return select_row<POOL / 16>(pool, hist, c, cnt, thr, eps, K, u);
 }
 
+// Bitonic network in which every compare-exchange has the same direction: the first step of
+// each merge pairs element i with its mirror i ^ (kk - 1) inside the 2S-block, the following
+// steps pair i with i ^ jj; the lower element index keeps the larger key. Element i sits in
+// lane u = i / EPL, register m = i % EPL. Partners inside the lane are registers; across
+// lanes they are one DPP move (mirror: lane u ^ 1/3/7/15 and element EPL-1-m; xor: u ^
+// 1/2/4/8). x = partner distance (i ^ x), kk = merge block (mirror steps only).
+template <int EPL>
+__device__ __forceinline__ void bitonic_stage(uint64_t (&key)[EPL], int kk, int x, bool mirror, int u)
+{
+    if (x < EPL) {
+#pragma unroll
+        for (int m = 0; m < EPL; ++m) {
+            const int m2 = m ^ x;
+            if (m2 <= m) continue;
+            const uint64_t a = key[m], b = key[m2];
+            const bool gt = a > b;
+            key[m] = gt ? a : b;
+            key[m2] = gt ? b : a;
+        }
+    } else {
+        const int lx = x / EPL;                           // partner lane = u ^ lx
+        const int hb = mirror ? (kk / EPL) >> 1 : lx;     // lane bit of the pair's top index bit
+        const bool keep_max = (u & hb) == 0;
+        uint64_t other[EPL];
+#pragma unroll
+        for (int m = 0; m < EPL; ++m) other[m] = lane_xor16_u64(key[mirror ? EPL - 1 - m : m], lx, u);
+#pragma unroll
+        for (int m = 0; m < EPL; ++m) {
+            const bool gt = key[m] > other[m];
+            key[m] = gt == keep_max ? key[m] : other[m];
+        }
+    }
+}
+
+// sorts every group of N consecutive elements (N / EPL lanes) into descending order
+template <int EPL, int N>
+__device__ __forceinline__ void bitonic_sort(uint64_t (&key)[EPL], int u)
+{
+#pragma unroll
+    for (int kk = 2; kk <= N; kk <<= 1) {
+#pragma unroll
+        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+            const bool mirror = jj == (kk >> 1);
+            bitonic_stage<EPL>(key, kk, mirror ? kk - 1 : jj, mirror, u);
+        }
+    }
+}
+
+// sorts a bitonic group of N elements (descending, then ascending) into descending order
+template <int EPL, int N>
+__device__ __forceinline__ void bitonic_merge(uint64_t (&key)[EPL], int u)
+{
+#pragma unroll
+    for (int jj = N >> 1; jj > 0; jj >>= 1) bitonic_stage<EPL>(key, N, jj, false, u);
+}
+
+template <int KP2>
+__device__ void write_row(const uint64_t (&key)[KP2 / 16], int kept, int64_t row, int64_t T,
+                          int64_t k_eff, int32_t* out_idx, float* out_scores, int u);
+
 // Sort row r's (exactly scored) winners into canonical order and write them plus pads.
 // `row` is the query position t in its batch; out_idx/out_scores point at the batch.
 template <int KP2, int POOL>
@@ -614,42 +674,52 @@ __device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
         const uint2 en = reinterpret_cast<const uint2*>(pool)[i];
         key[m] = i < kept ? make_key(__uint_as_float(en.x), en.y) : 0ull;
     }
-    // Bitonic sort into descending order in which every compare-exchange has the same
-    // direction: the first step of each merge pairs element i with its mirror i ^ (kk - 1)
-    // inside the 2S-block, the following steps pair i with i ^ jj; the lower element index
-    // keeps the larger key. Partners inside the lane are registers; across lanes they are
-    // one DPP move (mirror: lane u ^ 1/3/7/15 and element EPL-1-m; xor: u ^ 1/2/4/8).
+    bitonic_sort<EPL, KP2>(key, u);
+    write_row<KP2>(key, kept, row, T, k_eff, out_idx, out_scores, u);
+}
+
+// Exact selection fused into the sort, for K in (64, 128] and c <= 144 exactly scored
+// entries (after the final prune a K = 128 pool holds ~135): A = slots 0..127 is sorted
+// descending and B = slots 128..c-1 (at most 16, in lanes 14 and 15) descending; then
+// C[i] = max(A[i], B[127 - i]) holds the 128 largest of A and B as a bitonic sequence
+// (A falls, the reversed B rises), and one bitonic merge sorts it. This replaces the radix
+// select's histogram rounds with a 16-element sort, one exchange and seven merge steps.
+template <int POOL>
+__device__ void emit_row_merge(const Entry* pool, int c, int64_t row, int64_t T, int64_t k_eff,
+                               int32_t* out_idx, float* out_scores, int u)
+{
+    constexpr int KP2 = 128, EPL = 8, NB = 16;
+    static_assert(POOL >= KP2 + NB, "pool too small");
+    uint64_t key[EPL], bkey[EPL];
 #pragma unroll
-    for (int kk = 2; kk <= KP2; kk <<= 1) {
-#pragma unroll
-        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-            const bool mirror = jj == (kk >> 1);
-            const int x = mirror ? kk - 1 : jj;   // partner index = i ^ x
-            if (x < EPL) {
-#pragma unroll
-                for (int m = 0; m < EPL; ++m) {
-                    const int m2 = m ^ x;
-                    if (m2 <= m) continue;
-                    const uint64_t a = key[m], b = key[m2];
-                    const bool gt = a > b;
-                    key[m] = gt ? a : b;
-                    key[m2] = gt ? b : a;
-                }
-            } else {
-                const int lx = x / EPL;                           // partner lane = u ^ lx
-                const int hb = mirror ? (kk / EPL) >> 1 : lx;     // lane bit of the pair's top index bit
-                const bool keep_max = (u & hb) == 0;
-                uint64_t other[EPL];
-#pragma unroll
-                for (int m = 0; m < EPL; ++m) other[m] = lane_xor16_u64(key[mirror ? EPL - 1 - m : m], lx, u);
-#pragma unroll
-                for (int m = 0; m < EPL; ++m) {
-                    const bool gt = key[m] > other[m];
-                    key[m] = gt == keep_max ? key[m] : other[m];
-                }
-            }
-        }
+    for (int m = 0; m < EPL; ++m) {
+        const int i = u * EPL + m;   // reads are unconditional (slots < KP2 + NB <= POOL), masked
+        const uint2 ea = reinterpret_cast<const uint2*>(pool)[i];
+        key[m] = i < c ? make_key(__uint_as_float(ea.x), ea.y) : 0ull;
+        const int jb = i - (KP2 - NB);   // B entry of element i of lanes 14 and 15
+        const int sb = KP2 + (jb < 0 ? 0 : jb);
+        const uint2 eb = reinterpret_cast<const uint2*>(pool)[sb];
+        bkey[m] = jb >= 0 && sb < c ? make_key(__uint_as_float(eb.x), eb.y) : 0ull;
     }
+    bitonic_sort<EPL, KP2>(key, u);
+    bitonic_sort<EPL, NB>(bkey, u);   // lane 14: B[0..7], lane 15: B[8..15]; other lanes 0
+    // B[127 - i] for element i = 8u + m of lanes 14 and 15 is element 7 - m of the other lane
+    // of the pair; the other lanes pair with lanes whose B keys are 0
+#pragma unroll
+    for (int m = 0; m < EPL; ++m) {
+        const uint64_t o = lane_xor16_u64(bkey[EPL - 1 - m], 1, u);
+        key[m] = o > key[m] ? o : key[m];
+    }
+    bitonic_merge<EPL, KP2>(key, u);
+    write_row<KP2>(key, c < KP2 ? c : KP2, row, T, k_eff, out_idx, out_scores, u);
+}
+
+// Write a row's sorted keys (the first `kept` are winners) and the pads after them.
+template <int KP2>
+__device__ void write_row(const uint64_t (&key)[KP2 / 16], int kept, int64_t row, int64_t T,
+                          int64_t k_eff, int32_t* out_idx, float* out_scores, int u)
+{
+    constexpr int EPL = KP2 / 16;
     int32_t* oi = out_idx + row * k_eff;
     float* os = out_scores ? out_scores + row * k_eff : nullptr;
     if (kept == KP2 && k_eff == KP2 && !os && (reinterpret_cast<uintptr_t>(oi) & 15u) == 0) {
@@ -957,17 +1027,32 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
 #endif
     const int cw2 = wave_max_of_rows(c);   // counts after the prune, every lane of the wave
     if (row_live) {
-        const int kept = exact_row<DT, VEC, RP, POOL, (KP2 <= 128)>(sm.pool[rr], sm.hist[rr], c, cw2,
-                                                                   sm.cnt[rr], sm.thr[rr], sm.eps[rr],
-                                                                   sm.q[rr], kb, p.kst, p.ksr, R, K, u);
+        int32_t* const oidx = p.out_idx + b * T * p.k_eff;
 #ifdef WF_TOPK_TIMING
-        tmB = wall_clock64();
-        emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, p.out_idx + b * T * p.k_eff,
-                            nullptr, u);
+        float* const oscr = nullptr;   // out_scores carries the timestamps
 #else
-        emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, p.out_idx + b * T * p.k_eff,
-                            p.out_scores ? p.out_scores + b * T * p.k_eff : nullptr, u);
+        float* const oscr = p.out_scores ? p.out_scores + b * T * p.k_eff : nullptr;
 #endif
+        bool done = false;
+        if constexpr (KP2 == 128) {
+            if (cw2 <= KP2 + 16) {   // wave-uniform: selection fused into the sort
+                rescore_row<DT, VEC, RP>(sm.pool[rr], c, sm.q[rr], kb, p.kst, p.ksr, R, u);
+#ifdef WF_TOPK_TIMING
+                tmB = wall_clock64();
+#endif
+                emit_row_merge<POOL>(sm.pool[rr], c, r0 + rr, T, p.k_eff, oidx, oscr, u);
+                done = true;
+            }
+        }
+        if (!done) {
+            const int kept = exact_row<DT, VEC, RP, POOL, (KP2 <= 128)>(sm.pool[rr], sm.hist[rr], c, cw2,
+                                                                       sm.cnt[rr], sm.thr[rr], sm.eps[rr],
+                                                                       sm.q[rr], kb, p.kst, p.ksr, R, K, u);
+#ifdef WF_TOPK_TIMING
+            tmB = wall_clock64();
+#endif
+            emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, oidx, oscr, u);
+        }
     }
 #ifdef WF_TOPK_TIMING
     const uint64_t tmC = wall_clock64();
