@@ -461,7 +461,9 @@ __device__ void rescore_row(Entry* pool, int c, const float* q, const DT* kb, in
     if constexpr (VEC) {   // R == RP: every chunk lies inside the row
         constexpr int NC = RP / 8;
         constexpr int U4 = NC * (sizeof(DT) == 4 ? 2 : 1);   // 16-byte loads per key row
-        constexpr int NBR = U4 >= 16 ? 1 : 16 / U4;
+        // key rows in flight per lane: 2 for 16-bit keys at R = 32 (measured faster than 4:
+        // the phase is bound by its VALU work, not by load round trips), else 16 / U4
+        constexpr int NBR = U4 >= 16 ? 1 : (U4 == 4 ? 2 : 16 / U4);
         for (int e0 = 0; e0 < c; e0 += 16 * NBR) {
             uint4 lo[NBR][NC], hi[NBR][NC];
 #pragma unroll
