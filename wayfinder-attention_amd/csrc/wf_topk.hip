@@ -22,6 +22,8 @@
 //              (score desc, index asc) are radix-selected from the 64-bit keys.
 //  4. emit     The K winners are bitonic-sorted into canonical order and written with
 //              the reference's pad indices for rows that have fewer than K causal keys.
+//              For 64 < K <= 128 with at most K + 16 entries left after the final prune,
+//              the selection of step 3 and this sort are one network (emit_row_merge).
 //
 // Exactness: let E be the exact top-K of the keys seen so far and s_K its K-th score. The
 // pool always contains E: a pool holding K entries with MFMA score >= theta' has exact
