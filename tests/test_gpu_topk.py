@@ -101,6 +101,20 @@ def test_topk_all_ties(device):
     assert idx[0, -1].tolist() == list(range(K))
 
 
+@pytest.mark.parametrize("K,T", [(128, 3000), (100, 2500)])
+def test_topk_quantized_score_ties(device, K, T):
+    """Addresses in {-1, 0, 1}: every score is a small integer, so each row's K-th place
+    falls inside a large group of equal scores and the lower-index rule decides the set.
+    Covers the final selection fused into the sort (64 < K <= 128, pools of K..K+16
+    entries) and the radix select alike."""
+    _say(f"[topk] quantized ties K={K} T={T}")
+    g = torch.Generator().manual_seed(4242 + K)
+    B, R = 2, 32
+    qa = torch.randint(-1, 2, (B, T, R), generator=g).to(torch.bfloat16)
+    ka = torch.randint(-1, 2, (B, T, R), generator=g).to(torch.bfloat16)
+    _check_exact(qa, ka, K, device)
+
+
 def test_topk_short_sequence_wraps_pads(device):
     _say("[topk] T < K")
     qa, ka = addresses(2, 50, 32, seed=8, dtype=torch.bfloat16)
