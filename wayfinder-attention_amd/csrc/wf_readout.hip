@@ -380,12 +380,18 @@ void sparse_readout_fast(ReadoutParams p)
     load_idx(jA);
     gather(jA, kAlo, kAhi, vAlo, vAhi);
     load_idx(jB);
+    // the load-issuing stretches run at wave priority 1, so a wave about to issue its
+    // gathers is picked ahead of waves in their arithmetic (config 5 readout -1.3 %)
     for (int tau = 0; tau < ntask; tau += 2) {
+        __builtin_amdgcn_s_setprio(1);
         load_idx(jA);
         gather(jB, kBlo, kBhi, vBlo, vBhi);
+        __builtin_amdgcn_s_setprio(0);
         compute(kAlo, kAhi, vAlo, vAhi);
+        __builtin_amdgcn_s_setprio(1);
         load_idx(jB);
         gather(jA, kAlo, kAhi, vAlo, vAhi);
+        __builtin_amdgcn_s_setprio(0);
         if (tau + 1 < ntask) compute(kBlo, kBhi, vBlo, vBhi);
     }
 }
