@@ -589,8 +589,9 @@ __device__ int select_row(Entry* pool, uint32_t* hist, int c, int& cnt, float& t
 // kept (uniform over the row); lane u == 0 stores cnt and the exact threshold s_K - eps.
 // The selection reads ceil(cw / 16) entries per lane, cw >= c being the fullest pool among
 // the wave's rows (wave-uniform, so the wave takes one branch): after a final prune a
-// K = 128 pool holds ~135 entries. SIZED adds the 9-entry variant (K <= 128 kernels; the
-// K = 256 ones stay within their register budget without it).
+// K = 128 pool holds ~135 entries. SIZED adds the 9-entry variant (K <= 128 kernels); the
+// K = 256 kernels read 20 entries per lane when the wave's pools hold at most 320 (a final
+// K = 256 pool holds ~290 entries).
 template <typename DT, bool VEC, int RP, int POOL, bool SIZED>
 __device__ int exact_row(Entry* pool, uint32_t* hist, int c, int cw, int& cnt, float& thr,
                          float eps, const float* q, const DT* kb, int64_t kst, int64_t ksr, int R,
@@ -599,6 +600,8 @@ __device__ int exact_row(Entry* pool, uint32_t* hist, int c, int cw, int& cnt, f
     rescore_row<DT, VEC, RP>(pool, c, q, kb, kst, ksr, R, u);
     if constexpr (SIZED) {
         if (cw <= 16 * 9) return select_row<9>(pool, hist, c, cnt, thr, eps, K, u);
+    } else {
+        if (cw <= 16 * 20) return select_row<20>(pool, hist, c, cnt, thr, eps, K, u);
     }
     if (cw <= 16 * 12) return select_row<12>(pool, hist, c, cnt, thr, eps, K, u);
     return select_row<POOL / 16>(pool, hist, c, cnt, thr, eps, K, u);
