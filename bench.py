@@ -6,11 +6,13 @@ resident in HBM; q/k/v in the attention module's natural (B,T,H,D) memory viewed
 (B,H,T,D). One step = one fused_sparse_attention call (retrieval + readout, both HIP
 kernels of libwayfinder_hip.so).
 
-Prints ONE JSON line: latency (ms) as `value`, a `roofline` object for the dominant kernel
-(the readout: algorithmic bytes / its HIP-event-timed duration vs 8 TB/s), a
-`cpu_baseline` object (the reference's op sequence restated in PyTorch-CPU on this host,
-timed on a bounded sample and scaled to the full call), and the dense causal SDPA
-comparator at the same shape on the same GPU.
+Prints ONE JSON line: latency (ms) as `value`; a `roofline` object for the dominant kernel
+(the readout): HBM bytes per launch measured with rocprofv3 counters (profiles/) over its
+HIP-event time against the 8 TB/s peak, beside the readout's time against its measured
+gather-path bound (the same loads without arithmetic, wf_probe_gather) and the
+gather-inclusive algorithmic byte rate; a `cpu_baseline` object (the reference's op
+sequence restated in PyTorch-CPU on this host's cores: 1 warm-up and 3 timed runs of the
+whole call); and the dense causal SDPA comparator at the same shape on the same GPU.
 """
 
 from __future__ import annotations
@@ -87,8 +89,9 @@ def time_loop(fn, steps, warmup):
     return start.elapsed_time(stop) / steps
 
 
-def per_call_ms(fn, reps):
-    """Median / min / p90 of single-call HIP-event times."""
+def per_call_samples(fn, reps):
+    """Single-call HIP-event times (the device synchronised between calls): mean, median,
+    min and p90 of one sample set."""
     ts = []
     for _ in range(reps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -98,44 +101,53 @@ def per_call_ms(fn, reps):
         torch.cuda.synchronize()
         ts.append(a.elapsed_time(b))
     ts.sort()
-    return statistics.median(ts), ts[0], ts[int(0.9 * (len(ts) - 1))]
+    return {"mean": round(statistics.fmean(ts), 4), "median": round(statistics.median(ts), 4),
+            "min": round(ts[0], 4), "p90": round(ts[int(0.9 * (len(ts) - 1))], 4), "samples": reps}
 
 
-def cpu_baseline(cpu, cfg, rows_readout=512):
+def cpu_baseline(cpu, cfg, chunk=1024, runs=3):
     """The reference path restated op by op in PyTorch-CPU (oracle/torch_reference.py) on
-    this host's cores: retrieval on the reference's last row block (rows T-block..T, the
-    full causal prefix), readout on the last `rows_readout` query rows; each scaled to the
-    whole call (retrieval by the triangular sum of the row blocks, readout by T/rows)."""
+    all of this host's cores, on the whole call: the retrieval over every row block, then
+    the readout in chunks of `chunk` query rows (the gathered (B,H,rows,K,D) K/V of the
+    reference's readout do not fit in memory at once at config 5). One warm-up run, then
+    `runs` timed runs; median / min / max per stage and of their sum."""
     from oracle import torch_reference as tr
 
     B, H, T, D, R, K, dtype, _ = cfg
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
-    bm = tr._row_block(T)
-    blocks = [(i0, min(i0 + bm, T)) for i0 in range(0, T, bm)]
-    i0, i1 = blocks[-1]
-    # warm the thread pool on a tiny problem
-    tr.row_blocked_topk(cpu["qa"][:, :256], cpu["ka"][:, :256], K)
-    t0 = time.perf_counter()
-    idx = tr.row_blocked_topk(cpu["qa"], cpu["ka"], K, row_range=(i0, i1))
-    t_ret = time.perf_counter() - t0
-    ret_scale = sum((b1 - b0) * b1 for b0, b1 in blocks) / ((i1 - i0) * i1)
-    r0 = T - rows_readout
-    q = cpu["q"][:, :, r0:]
-    sub_idx = idx[:, r0:]
-    # gather on the full k/v, readout rows [r0, T) only
-    t0 = time.perf_counter()
-    tr.sparse_meat_reference(q, cpu["k"], cpu["v"], sub_idx, D ** -0.5)
-    t_read = time.perf_counter() - t0
-    total_ms = (t_ret * ret_scale + t_read * T / rows_readout) * 1e3
+    scale = D ** -0.5
+
+    def retrieval():
+        return tr.row_blocked_topk(cpu["qa"], cpu["ka"], K)
+
+    def readout(idx):
+        for r0 in range(0, T, chunk):
+            r1 = min(T, r0 + chunk)
+            tr.sparse_meat_reference(cpu["q"][:, :, r0:r1], cpu["k"], cpu["v"], idx[:, r0:r1], scale)
+
+    ret_t, read_t = [], []
+    for it in range(runs + 1):        # run 0 is the warm-up
+        t0 = time.perf_counter()
+        idx = retrieval()
+        t1 = time.perf_counter()
+        readout(idx)
+        t2 = time.perf_counter()
+        if it:
+            ret_t.append((t1 - t0) * 1e3)
+            read_t.append((t2 - t1) * 1e3)
+    tot = [a + b for a, b in zip(ret_t, read_t)]
+
+    def stats(v):
+        return {"median": round(statistics.median(v), 2), "min": round(min(v), 2), "max": round(max(v), 2)}
+
     return {
-        "value": round(total_ms, 2), "unit": "ms", "cores": torch.get_num_threads(),
+        "value": round(statistics.median(tot), 2), "unit": "ms", "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"torch-CPU restatement of the reference path; retrieval timed on row block "
-                   f"[{i0},{i1}) x{ret_scale:.3f} ({t_ret * 1e3:.0f} ms), readout on rows "
-                   f"[{r0},{T}) x{T // rows_readout} ({t_read * 1e3:.0f} ms); one timed run each"),
-        "retrieval_ms": round(t_ret * ret_scale * 1e3, 2),
-        "readout_ms": round(t_read * T / rows_readout * 1e3, 2),
+        "sample": (f"whole call (no sampling): torch-CPU restatement of the reference path, retrieval "
+                   f"over all {-(-T // tr._row_block(T))} row blocks of {tr._row_block(T)}, readout in "
+                   f"chunks of {chunk} query rows; 1 warm-up + {runs} timed runs, median"),
+        "total_ms": stats(tot), "retrieval_ms": stats(ret_t), "readout_ms": stats(read_t),
         "cpu_model": _cpu_model(),
     }
 
@@ -148,6 +160,30 @@ def _cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def gather_probe_fn(dev, idx):
+    """A callable running wf_probe_gather over the readout's inputs: the readout's index
+    loads and K/V gathers without its arithmetic (its time bounds the readout's)."""
+    import ctypes
+
+    from routing_attention.kernels import _lib
+
+    lib = _lib.load()
+    k, v = dev["k"], dev["v"]
+    B, H, T, D = k.shape
+    K = idx.shape[-1]
+    nbytes = lib.wf_probe_gather_sink_bytes(B, H, T)
+    sink = torch.empty(max(nbytes // 4, 1), dtype=torch.int32, device=k.device)
+    ks, vs, is_ = _lib.strides(k), _lib.strides(v), _lib.strides(idx)
+    stream = _lib.stream_ptr(k.device)
+    code = _lib.dtype_code(k)
+
+    def run():
+        _lib.check(lib.wf_probe_gather(k.data_ptr(), v.data_ptr(), code, B, H, T, D, ks, vs,
+                                       idx.data_ptr(), is_, K, ctypes.c_void_p(sink.data_ptr()),
+                                       nbytes, stream))
+    return run
 
 
 def run_leg(args, dev, K, scale, readout_bytes):
@@ -178,6 +214,17 @@ def run_leg(args, dev, K, scale, readout_bytes):
                            args.steps, args.warmup)
         print(json.dumps({"leg": "backward", "ms": round(ms, 4), "fwd_lse_ms": round(fwd_ms, 4),
                           "gathered_gbs": round(2 * (readout_bytes) / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return
+    if args.leg == "gather":
+        probe = gather_probe_fn(dev, idx)
+        ms_probe = time_loop(probe, args.steps, args.warmup)
+        ms_read = time_loop(lambda: sparse_meat_attention(dev["q"], dev["k"], dev["v"], idx, scale),
+                            args.steps, args.warmup)
+        B, H, T, D = dev["k"].shape
+        gathered = 2 * B * H * T * idx.shape[-1] * D * dev["k"].element_size()
+        print(json.dumps({"leg": "gather", "probe_ms": round(ms_probe, 4), "readout_ms": round(ms_read, 4),
+                          "readout_frac_of_gather_bound": round(ms_probe / ms_read, 4),
+                          "probe_gathered_gbs": round(gathered / (ms_probe * 1e-3) / 1e9, 1)}), flush=True)
         return
     fn = lambda: sparse_meat_attention(dev["q"], dev["k"], dev["v"], idx, scale)  # noqa: E731
     ms = time_loop(fn, args.steps, args.warmup)
@@ -223,7 +270,7 @@ def bench_decoder(args):
     base = torch.cuda.memory_allocated()
     ms = time_loop(step, args.steps, args.warmup)
     peak_mb = (torch.cuda.max_memory_allocated() - base) / 2 ** 20
-    med, mn, p90 = per_call_ms(step, max(10, args.steps // 2))
+    lat = per_call_samples(step, max(10, args.steps // 2))
     # the same forward captured once as a HIP graph and replayed (serving loops): the
     # launches of the ~60 kernels per forward go out as one graph launch
     side = torch.cuda.Stream()
@@ -252,8 +299,8 @@ def bench_decoder(args):
         "data": "synthetic (random-init weights, tokens uniform over the vocabulary from a seed)",
         "config": {"workload": "config 2: 4-layer decoder forward", **c,
                    "attention": "learned_address, fused HIP top-K + readout", "parallelism": "single GPU"},
-        "latency_ms": {"mean": round(ms, 4), "median": round(med, 4), "min": round(mn, 4),
-                       "p90": round(p90, 4)},
+        "latency_ms": lat,
+        "pipelined_ms_per_call": round(ms, 4),
         "peak_mb": round(peak_mb, 1),
         "graph_replay_ms_per_step": round(gms, 4),
         "graph_replay_tokens_per_s": round(tokens / (gms * 1e-3), 1),
@@ -273,9 +320,11 @@ def main():
                     help="c4 (default) is the metric's workload; c2 times the 4-layer decoder")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
-    ap.add_argument("--leg", default="all", choices=["all", "topk", "readout", "backward", "copy"],
+    ap.add_argument("--cpu-runs", type=int, default=3, help="timed runs of the CPU baseline")
+    ap.add_argument("--leg", default="all", choices=["all", "topk", "readout", "backward", "copy", "gather"],
                     help="profiling aid: run only one kernel (or a 256 MiB device copy used to "
-                         "calibrate the FETCH_SIZE / WRITE_SIZE counters) and print its timing")
+                         "calibrate the FETCH_SIZE / WRITE_SIZE counters, or the readout against "
+                         "its gather-path probe) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this path has no multi-GPU code "
@@ -303,19 +352,29 @@ def main():
         run_leg(args, dev, K, scale, readout_bytes)
         return
 
+    # peak extra HBM of one call with nothing else live (output + indices + workspace)
+    torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base_mem = torch.cuda.memory_allocated()
-    _, idx = step()
+    res = step()
     torch.cuda.synchronize()
-    ms = time_loop(step, args.steps, args.warmup)
     peak_mb = (torch.cuda.max_memory_allocated() - base_mem) / 2 ** 20
-    med, mn, p90 = per_call_ms(step, max(10, args.steps // 2))
+    idx = res[1]
+    del res
 
-    # per-kernel legs (same kernels as inside the fused call)
+    # the metric: `steps` back-to-back calls between two events (value / ms_per_step)
+    ms = time_loop(step, args.steps, args.warmup)
+    # per-call latency: every statistic from the same set of single-call event samples
+    lat = per_call_samples(step, max(10, args.steps // 2))
+
+    # per-kernel legs (the kernels of the fused call, each timed alone with HIP events on
+    # the stream they run on) and the readout's gather-path bound
     ms_topk = time_loop(lambda: causal_topk(dev["qa"], dev["ka"], K), args.steps, 3)
     ms_read = time_loop(lambda: sparse_meat_attention(dev["q"], dev["k"], dev["v"], idx, scale),
                         args.steps, 3)
-    read_gbs = readout_bytes / (ms_read * 1e-3) / 1e9
+    ms_probe = time_loop(gather_probe_fn(dev, idx), args.steps, 3)
+    k_eff = min(K, T)
+    gathered = 2 * B * H * T * k_eff * D * s
     score_flops = B * R * T * (T + 1)
 
     dense = None
@@ -326,14 +385,15 @@ def main():
         fn = lambda: F.scaled_dot_product_attention(qd, kd, vd, is_causal=True, scale=scale)  # noqa: E731
         fn()
         torch.cuda.synchronize()
-        dmed, dmin, dp90 = per_call_ms(fn, 50)
-        dense = {"median_ms": round(dmed, 4), "min_ms": round(dmin, 4), "p90_ms": round(dp90, 4),
+        dl = per_call_samples(fn, 50)
+        dense = {"median_ms": dl["median"], "min_ms": dl["min"], "p90_ms": dl["p90"],
                  "peak_mb": round((torch.cuda.max_memory_allocated() - m0) / 2 ** 20, 1)}
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", f"readout_traffic_{args.config}.json")
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+    hbm_gbs = traffic / (ms_read * 1e-3) / 1e9 if traffic else None
 
     line = {
         "metric": "fused top-K128+sparse-attn fwd latency (ms) @T=16384; % HBM roofline",
@@ -351,17 +411,31 @@ def main():
         "config": {"workload": f"fused causal top-K + sparse attention fwd, config {args.config[1:]}",
                    "B": B, "H": H, "T": T, "head_dim": D, "d_A": R, "top_k": K,
                    "qkv_memory": "(B,T,H,D)", "parallelism": "single GPU"},
-        "latency_ms": {"mean": round(ms, 4), "median": round(med, 4), "min": round(mn, 4),
-                       "p90": round(p90, 4)},
+        "latency_ms": lat,
+        "pipelined_ms_per_call": round(ms, 4),
         "rows_per_s": round(B * T / (ms * 1e-3), 1),
-        "kernels_ms": {"causal_topk": round(ms_topk, 4), "sparse_readout": round(ms_read, 4)},
+        "kernels_ms": {"causal_topk": round(ms_topk, 4), "sparse_readout": round(ms_read, 4),
+                       "gather_probe": round(ms_probe, 4)},
+        # dominant kernel: the readout. achieved = its HBM bytes per launch (rocprofv3
+        # FETCH_SIZE + WRITE_SIZE, calibrated on a device copy) / its HIP-event time
         "roofline": {"bound": "hbm", "kernel": "sparse_readout_fast",
-                     "achieved": round(read_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(read_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": readout_bytes},
-        "path_roofline": {"algorithmic_bytes": path_bytes,
-                          "achieved_gbs": round(path_bytes / (ms * 1e-3) / 1e9, 1),
-                          "frac": round(path_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+                     "achieved": round(hbm_gbs, 1) if hbm_gbs else None, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(hbm_gbs / HBM_PEAK_GBS, 4) if hbm_gbs else None,
+                     "traffic": traffic,
+                     "basis": "counter-measured HBM bytes per launch / readout event time",
+                     # what binds it: the gathers themselves (mostly L2 hits); the probe issues
+                     # the same loads with no arithmetic
+                     "gather_path": {"probe_ms": round(ms_probe, 4), "readout_ms": round(ms_read, 4),
+                                     "frac": round(ms_probe / ms_read, 4),
+                                     "probe_gathered_gbs": round(gathered / (ms_probe * 1e-3) / 1e9, 1)},
+                     # SURVEY 8(d)'s count: one K and one V row per (query, head, neighbour)
+                     "algorithmic_gather_inclusive": {
+                         "bytes": readout_bytes,
+                         "gbs": round(readout_bytes / (ms_read * 1e-3) / 1e9, 1),
+                         "x_hbm_peak": round(readout_bytes / (ms_read * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}},
+        "path_algorithmic": {"bytes": path_bytes,
+                             "gbs": round(path_bytes / (ms * 1e-3) / 1e9, 1),
+                             "x_hbm_peak": round(path_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)},
         # the retrieval's score contraction (q_addr . k_addr over the causal triangle,
         # B*d_A*T*(T+1) flops) against the dense MFMA peak: it is far from that bound
         "retrieval_mfma": {"kernel": "causal_topk_kernel", "flops": score_flops,
@@ -370,10 +444,10 @@ def main():
                            "frac": round(score_flops / (ms_topk * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS[dtype], 5)},
         "peak_mb": round(peak_mb, 1),
         "dense_causal_sdpa": dense,
-        "vs_dense": round(dense["median_ms"] / med, 3) if dense else None,
+        "vs_dense": round(dense["median_ms"] / lat["median"], 3) if dense else None,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cpu, cfg)
+        line["cpu_baseline"] = cpu_baseline(cpu, cfg, runs=args.cpu_runs)
     print(json.dumps(line), flush=True)
 
 

@@ -226,6 +226,21 @@ size_t wf_fused_workspace_bytes(int64_t B, int64_t T, int64_t R, int64_t top_k);
  */
 int wf_fused_topk_sparse_fwd(const wf_fused_args* args, void* stream);
 
+/*
+ * Measurement aid, no reference counterpart: the readout's gather path with no arithmetic.
+ * Issues exactly the loads of wf_sparse_readout_fwd's fast kernel (same grid, workgroup
+ * order, 16-byte index loads and K/V row gathers, two tasks in flight per wave) and folds
+ * the loaded words into one XOR per lane written to `sink`, so its time is the speed of
+ * light of the readout's memory pattern. k, v: (B, H, T, D) bf16/f16 in the readout's fast
+ * layout; indices (B, T, K) int32 with contiguous, 16-byte aligned rows, K % 4 == 0 (entries
+ * are clamped to [0, T-1]); sink: >= wf_probe_gather_sink_bytes(B, H, T) bytes.
+ */
+size_t wf_probe_gather_sink_bytes(int64_t B, int64_t H, int64_t T);
+int wf_probe_gather(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t T,
+                    int64_t D, const int64_t* k_strides, const int64_t* v_strides,
+                    const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                    uint32_t* sink, size_t sink_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,11 +37,18 @@ def lib() -> ctypes.CDLL:
         l.wfo_causal_topk_rows.restype = None
         l.wfo_causal_topk_rows.argtypes = [_ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64,
                                            _i64, _ptr, _ptr]
+        l.wfo_causal_topk_rowlist.restype = None
+        l.wfo_causal_topk_rowlist.argtypes = [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64,
+                                              _ptr, _ptr]
         l.wfo_causal_topk.restype = None
         l.wfo_causal_topk.argtypes = [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _ptr]
         l.wfo_sparse_readout.restype = None
         l.wfo_sparse_readout.argtypes = [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
                                          _i64, ctypes.c_float, ctypes.c_uint, _ptr]
+        l.wfo_sparse_readout_rows.restype = None
+        l.wfo_sparse_readout_rows.argtypes = [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
+                                              _i64, _ptr, _i64, ctypes.c_float, ctypes.c_uint,
+                                              _ptr]
         _lib = l
     return _lib
 
@@ -94,6 +101,22 @@ def causal_topk_rows(query, key, top_k: int, b: int, row0: int, row1: int,
     return (idx_t, torch.from_numpy(sc)) if return_scores else idx_t
 
 
+def causal_topk_rowlist(query, key, top_k: int, rows_bt, *, return_scores: bool = False):
+    """Selected (b, t) rows, rows_bt (n, 2) int: (n, k_eff) canonical indices (+ scores)."""
+    q = _f32(query)
+    k = _f32(key)
+    B, T, R = q.shape
+    k_eff = min(int(top_k), T)
+    rb = np.ascontiguousarray(torch.as_tensor(rows_bt).to(torch.int64).numpy(), dtype=np.int64)
+    n = rb.shape[0]
+    idx = np.empty((n, k_eff), dtype=np.int32)
+    sc = np.empty((n, k_eff), dtype=np.float32)
+    if k_eff > 0 and n > 0:
+        lib().wfo_causal_topk_rowlist(_p(q), _p(k), B, T, R, int(top_k), _p(rb), n, _p(idx), _p(sc))
+    idx_t = torch.from_numpy(idx)
+    return (idx_t, torch.from_numpy(sc)) if return_scores else idx_t
+
+
 def sparse_readout(q, k, v, indices, scale: float, flags: int = 0) -> torch.Tensor:
     """(B,H,T,D) x3 + int32 (B,T,K) -> float64 (B,H,T,D)."""
     qn, kn, vn = _f32(q), _f32(k), _f32(v)
@@ -105,6 +128,22 @@ def sparse_readout(q, k, v, indices, scale: float, flags: int = 0) -> torch.Tens
     out = np.empty((B, H, T, D), dtype=np.float64)
     lib().wfo_sparse_readout(_p(qn), _p(kn), _p(vn), B, H, T, D, _p(idx), K,
                              float(scale), int(flags), _p(out))
+    return torch.from_numpy(out)
+
+
+def sparse_readout_rows(q, k, v, rows_bt, indices, scale: float, flags: int = 0) -> torch.Tensor:
+    """Readout of selected (b, t) rows only: rows_bt (n, 2) int, indices (n, K) int32 (the
+    index row of each pair) -> float64 (n, H, D). q, k, v (B,H,T,D) as in sparse_readout."""
+    qn, kn, vn = _f32(q), _f32(k), _f32(v)
+    B, H, T, D = qn.shape
+    rb = np.ascontiguousarray(torch.as_tensor(rows_bt).to(torch.int64).numpy(), dtype=np.int64)
+    idx = np.ascontiguousarray(torch.as_tensor(indices).cpu().to(torch.int32).numpy(), dtype=np.int32)
+    n, K = idx.shape
+    assert rb.shape == (n, 2)
+    out = np.empty((n, H, D), dtype=np.float64)
+    if n > 0:
+        lib().wfo_sparse_readout_rows(_p(qn), _p(kn), _p(vn), B, H, T, D, _p(rb), n, _p(idx), K,
+                                      float(scale), int(flags), _p(out))
     return torch.from_numpy(out)
 
 

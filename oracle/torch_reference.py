@@ -38,8 +38,8 @@ def _finalize(vals: torch.Tensor, idx: torch.Tensor, k_eff: int) -> torch.Tensor
     # causal_topk.py:37-57
     T = vals.shape[1]
     ok = torch.isfinite(vals) & (vals > -1e30)
-    t = torch.arange(T).view(1, T, 1)
-    s = torch.arange(k_eff).view(1, 1, k_eff)
+    t = torch.arange(T, device=vals.device).view(1, T, 1)
+    s = torch.arange(k_eff, device=vals.device).view(1, 1, k_eff)
     pad = (t + k_eff + s + 1) % T
     return torch.where(ok, idx.long(), pad).to(torch.int32)
 
@@ -47,8 +47,9 @@ def _finalize(vals: torch.Tensor, idx: torch.Tensor, k_eff: int) -> torch.Tensor
 @torch.no_grad()
 def row_blocked_topk(query: torch.Tensor, key: torch.Tensor, top_k: int,
                      row_range: tuple[int, int] | None = None) -> torch.Tensor:
-    """Reference retrieval on CPU. ``row_range`` restricts the work to the row blocks that
-    intersect [r0, r1) (used for bounded CPU-baseline samples); other rows are left -1."""
+    """Reference retrieval, on the device of ``query`` (the CPU for the baseline; a GPU for
+    the cross-check against torch's own GPU bmm / topk). ``row_range`` restricts the work
+    to the row blocks that intersect [r0, r1); other rows are left -1."""
     if query.shape != key.shape:
         raise ValueError(f"query/key shape mismatch: {query.shape} vs {key.shape}")
     if query.dim() != 3:
@@ -60,23 +61,24 @@ def row_blocked_topk(query: torch.Tensor, key: torch.Tensor, top_k: int,
     q, k = _promote(query, key)
     q, k = q.float(), k.float()
     bm = _row_block(T)
-    vals = torch.full((B, T, k_eff), float("-inf"))
-    idx = torch.full((B, T, k_eff), -1, dtype=torch.int32)
+    dev = q.device
+    vals = torch.full((B, T, k_eff), float("-inf"), device=dev)
+    idx = torch.full((B, T, k_eff), -1, dtype=torch.int32, device=dev)
     r0, r1 = row_range if row_range is not None else (0, T)
     for i0 in range(0, T, bm):
         i1 = min(i0 + bm, T)
         if i1 <= r0 or i0 >= r1:
             continue
         sc = torch.bmm(q[:, i0:i1], k[:, :i1].transpose(1, 2).contiguous())
-        rows = torch.arange(i0, i1).view(-1, 1)
-        cols = torch.arange(i1).view(1, -1)
+        rows = torch.arange(i0, i1, device=dev).view(-1, 1)
+        cols = torch.arange(i1, device=dev).view(1, -1)
         sc = sc.masked_fill((cols > rows).unsqueeze(0), float("-inf"))
         v, i = torch.topk(sc, k=k_eff, dim=-1, sorted=False)
         vals[:, i0:i1] = v
         idx[:, i0:i1] = i.to(torch.int32)
     out = _finalize(vals, idx, k_eff)
     if row_range is not None:
-        keep = torch.zeros(T, dtype=torch.bool)
+        keep = torch.zeros(T, dtype=torch.bool, device=dev)
         keep[r0:r1] = True
         out[:, ~keep] = -1
     return out

@@ -19,6 +19,7 @@
  *    ascending order, behaves the same). Output is canonical: score descending, then
  *    index ascending; valid keys fill slots 0..n_valid-1 and pads follow, which is the
  *    slot placement torch's GPU topk(sorted=False) gives rows whose tail is -inf.
+ *    wfo_causal_topk_rowlist: the same for an explicit list of (b, t) rows.
  *  - wfo_sparse_readout: sparse_meat_attention_reference
  *      routing_attention/kernels/fused_sparse.py:80-94 (gather k/v at indices shared
  *      across heads :64-77, scores = (q . k_sel) * scale, softmax, weighted sum of v_sel),
@@ -70,6 +71,44 @@ static int cmp_desc(const void* pa, const void* pb)
 }
 
 /*
+ * Row t of batch b: the k_eff best keys j <= t in canonical order, pads after them.
+ * heap: scratch of k_eff candidates. out_idx / out_score: k_eff entries (score may be NULL).
+ */
+static void topk_row(const float* qa, const float* ka, int64_t T, int64_t R, int64_t k_eff,
+                     int64_t b, int64_t t, cand* heap, int32_t* oi, float* os)
+{
+    const float* q = qa + (b * T + t) * R;
+    int64_t n = 0;
+    for (int64_t j = 0; j <= t; ++j) {
+        const float s = wfo_score(q, ka + (b * T + j) * R, R);
+        if (n < k_eff) {
+            /* insert and restore heap order upward */
+            int64_t i = n++;
+            heap[i].s = s; heap[i].j = (int32_t)j;
+            while (i > 0) {
+                int64_t p = (i - 1) / 2;
+                if (better(heap[p].s, heap[p].j, heap[i].s, heap[i].j)) {
+                    cand tmp = heap[p]; heap[p] = heap[i]; heap[i] = tmp; i = p;
+                } else break;
+            }
+        } else if (better(s, (int32_t)j, heap[0].s, heap[0].j)) {
+            heap[0].s = s; heap[0].j = (int32_t)j;
+            sift_down(heap, n, 0);
+        }
+    }
+    qsort(heap, (size_t)n, sizeof(cand), cmp_desc);
+    for (int64_t s = 0; s < k_eff; ++s) {
+        if (s < n) {
+            oi[s] = heap[s].j;
+            if (os) os[s] = heap[s].s;
+        } else {
+            oi[s] = (int32_t)((t + k_eff + s + 1) % T);
+            if (os) os[s] = -INFINITY;
+        }
+    }
+}
+
+/*
  * Rows [row0, row1) of batch b. qa, ka: contiguous (B, T, R) fp32.
  * out_idx / out_score: contiguous (row1 - row0, k_eff); out_score may be NULL.
  */
@@ -84,39 +123,31 @@ void wfo_causal_topk_rows(const float* qa, const float* ka, int64_t B, int64_t T
     {
         cand* heap = (cand*)malloc(sizeof(cand) * (size_t)k_eff);
 #pragma omp for schedule(dynamic, 16)
-        for (int64_t t = row0; t < row1; ++t) {
-            const float* q = qa + (b * T + t) * R;
-            int64_t n = 0;
-            for (int64_t j = 0; j <= t; ++j) {
-                const float s = wfo_score(q, ka + (b * T + j) * R, R);
-                if (n < k_eff) {
-                    /* insert and restore heap order upward */
-                    int64_t i = n++;
-                    heap[i].s = s; heap[i].j = (int32_t)j;
-                    while (i > 0) {
-                        int64_t p = (i - 1) / 2;
-                        if (better(heap[p].s, heap[p].j, heap[i].s, heap[i].j)) {
-                            cand tmp = heap[p]; heap[p] = heap[i]; heap[i] = tmp; i = p;
-                        } else break;
-                    }
-                } else if (better(s, (int32_t)j, heap[0].s, heap[0].j)) {
-                    heap[0].s = s; heap[0].j = (int32_t)j;
-                    sift_down(heap, n, 0);
-                }
-            }
-            qsort(heap, (size_t)n, sizeof(cand), cmp_desc);
-            int32_t* oi = out_idx + (t - row0) * k_eff;
-            float* os = out_score ? out_score + (t - row0) * k_eff : NULL;
-            for (int64_t s = 0; s < k_eff; ++s) {
-                if (s < n) {
-                    oi[s] = heap[s].j;
-                    if (os) os[s] = heap[s].s;
-                } else {
-                    oi[s] = (int32_t)((t + k_eff + s + 1) % T);
-                    if (os) os[s] = -INFINITY;
-                }
-            }
-        }
+        for (int64_t t = row0; t < row1; ++t)
+            topk_row(qa, ka, T, R, k_eff, b, t, heap, out_idx + (t - row0) * k_eff,
+                     out_score ? out_score + (t - row0) * k_eff : NULL);
+        free(heap);
+    }
+}
+
+/*
+ * Selected rows: rows_bt holds n pairs (b, t). out_idx / out_score: contiguous (n, k_eff);
+ * out_score may be NULL.
+ */
+void wfo_causal_topk_rowlist(const float* qa, const float* ka, int64_t B, int64_t T, int64_t R,
+                             int64_t top_k, const int64_t* rows_bt, int64_t n,
+                             int32_t* out_idx, float* out_score)
+{
+    (void)B;
+    const int64_t k_eff = top_k < T ? top_k : T;
+    if (k_eff <= 0) return;
+#pragma omp parallel
+    {
+        cand* heap = (cand*)malloc(sizeof(cand) * (size_t)k_eff);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t i = 0; i < n; ++i)
+            topk_row(qa, ka, T, R, k_eff, rows_bt[2 * i], rows_bt[2 * i + 1], heap,
+                     out_idx + i * k_eff, out_score ? out_score + i * k_eff : NULL);
         free(heap);
     }
 }
@@ -132,9 +163,48 @@ void wfo_causal_topk(const float* qa, const float* ka, int64_t B, int64_t T, int
 }
 
 /*
+ * One (b, h, t) row of the readout: softmax over the K slots of idx_row of
+ * scale * q[b,h,t] . k[b,h,j], weighted sum of v[b,h,j], accumulated in double.
+ * q, k, v: contiguous (B, H, T, D) fp32. sc / jj: scratch of K entries.
+ * flags bit 0: zero weight for slots s > t of rows t < K - 1 (pad slots of the retrieval).
+ */
+static void readout_row(const float* q, const float* k, const float* v, int64_t H, int64_t T,
+                        int64_t D, int64_t b, int64_t h, int64_t t, const int32_t* idx_row,
+                        int64_t K, float scale, unsigned flags, double* sc, int64_t* jj,
+                        double* orow)
+{
+    const int64_t bh = b * H + h;
+    const float* qr = q + (bh * T + t) * D;
+    double m = -INFINITY;
+    for (int64_t s = 0; s < K; ++s) {
+        int64_t j = idx_row[s];
+        if (j < 0) j += T;
+        if (j < 0) j = 0;
+        if (j > T - 1) j = T - 1;
+        jj[s] = j;
+        const int masked = (flags & 1u) && t < K - 1 && s > t;
+        if (masked) { sc[s] = -INFINITY; continue; }
+        const float* kr = k + (bh * T + j) * D;
+        double dot = 0.0;
+        for (int64_t d = 0; d < D; ++d) dot += (double)qr[d] * (double)kr[d];
+        sc[s] = dot * (double)scale;
+        if (sc[s] > m) m = sc[s];
+    }
+    for (int64_t d = 0; d < D; ++d) orow[d] = 0.0;
+    double l = 0.0;
+    for (int64_t s = 0; s < K; ++s) {
+        if (sc[s] == -INFINITY) continue;
+        const double p = exp(sc[s] - m);
+        l += p;
+        const float* vr = v + (bh * T + jj[s]) * D;
+        for (int64_t d = 0; d < D; ++d) orow[d] += p * (double)vr[d];
+    }
+    for (int64_t d = 0; d < D; ++d) orow[d] = l > 0.0 ? orow[d] / l : 0.0;
+}
+
+/*
  * q, k, v: contiguous (B, H, T, D) fp32; idx: contiguous (B, T, K) int32;
- * out: contiguous (B, H, T, D) double. flags bit 0: zero weight for slots s > t of
- * rows t < K - 1 (pad slots of the retrieval).
+ * out: contiguous (B, H, T, D) double (readout_row for every row).
  */
 void wfo_sparse_readout(const float* q, const float* k, const float* v,
                         int64_t B, int64_t H, int64_t T, int64_t D,
@@ -148,36 +218,35 @@ void wfo_sparse_readout(const float* q, const float* k, const float* v,
 #pragma omp for collapse(2) schedule(static)
         for (int64_t bh = 0; bh < B * H; ++bh) {
             for (int64_t t = 0; t < T; ++t) {
-                const int64_t b = bh / H;
-                const float* qr = q + (bh * T + t) * D;
-                const int32_t* ir = idx + (b * T + t) * K;
-                double m = -INFINITY;
-                for (int64_t s = 0; s < K; ++s) {
-                    int64_t j = ir[s];
-                    if (j < 0) j += T;
-                    if (j < 0) j = 0;
-                    if (j > T - 1) j = T - 1;
-                    jj[s] = j;
-                    const int masked = (flags & 1u) && t < K - 1 && s > t;
-                    if (masked) { sc[s] = -INFINITY; continue; }
-                    const float* kr = k + (bh * T + j) * D;
-                    double dot = 0.0;
-                    for (int64_t d = 0; d < D; ++d) dot += (double)qr[d] * (double)kr[d];
-                    sc[s] = dot * (double)scale;
-                    if (sc[s] > m) m = sc[s];
-                }
-                double* orow = out + (bh * T + t) * D;
-                for (int64_t d = 0; d < D; ++d) orow[d] = 0.0;
-                double l = 0.0;
-                for (int64_t s = 0; s < K; ++s) {
-                    if (sc[s] == -INFINITY) continue;
-                    const double p = exp(sc[s] - m);
-                    l += p;
-                    const float* vr = v + (bh * T + jj[s]) * D;
-                    for (int64_t d = 0; d < D; ++d) orow[d] += p * (double)vr[d];
-                }
-                for (int64_t d = 0; d < D; ++d) orow[d] = l > 0.0 ? orow[d] / l : 0.0;
+                const int64_t b = bh / H, h = bh % H;
+                readout_row(q, k, v, H, T, D, b, h, t, idx + (b * T + t) * K, K, scale, flags,
+                            sc, jj, out + (bh * T + t) * D);
             }
+        }
+        free(sc);
+        free(jj);
+    }
+}
+
+/*
+ * Selected rows only (cheap checks at full T): rows_bt holds n pairs (b, t); idx is
+ * contiguous (n, K) (the index row of each pair); out is contiguous (n, H, D) double.
+ */
+void wfo_sparse_readout_rows(const float* q, const float* k, const float* v,
+                             int64_t B, int64_t H, int64_t T, int64_t D,
+                             const int64_t* rows_bt, int64_t n, const int32_t* idx, int64_t K,
+                             float scale, unsigned flags, double* out)
+{
+    (void)B;
+#pragma omp parallel
+    {
+        double* sc = (double*)malloc(sizeof(double) * (size_t)(K > 0 ? K : 1));
+        int64_t* jj = (int64_t*)malloc(sizeof(int64_t) * (size_t)(K > 0 ? K : 1));
+#pragma omp for collapse(2) schedule(static)
+        for (int64_t i = 0; i < n; ++i) {
+            for (int64_t h = 0; h < H; ++h)
+                readout_row(q, k, v, H, T, D, rows_bt[2 * i], h, rows_bt[2 * i + 1], idx + i * K,
+                            K, scale, flags, sc, jj, out + (i * H + h) * D);
         }
         free(sc);
         free(jj);

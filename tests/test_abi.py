@@ -232,3 +232,18 @@ def test_address_contract_errors(lib, kw, code, msg):
 
 def test_address_empty_is_noop(lib):
     assert _addr(lib, B=0) == _lib.WF_OK
+
+
+def test_probe_gather_contract_errors(lib):
+    s4 = _i64(64 * 8 * 64, 64, 8 * 64, 1)
+    si = _i64(64 * 8, 8, 1)
+    call = lambda **kw: lib.wf_probe_gather(  # noqa: E731
+        kw.get("k", FAKE), FAKE, kw.get("dtype", 2), 1, 8, 64, kw.get("D", 64), s4, s4,
+        kw.get("idx", FAKE), si, kw.get("K", 8), FAKE, kw.get("sink", 1 << 20), None)
+    assert call(dtype=0) == _lib.WF_ERR_UNSUPPORTED and "16-bit" in _lib.last_error()
+    assert call(D=96) == _lib.WF_ERR_INVALID_ARGUMENT
+    assert call(K=6) == _lib.WF_ERR_UNSUPPORTED
+    assert call(k=None) == _lib.WF_ERR_INVALID_ARGUMENT
+    assert call(idx=FAKE + 4) == _lib.WF_ERR_UNSUPPORTED and "fast layout" in _lib.last_error()
+    assert call(sink=16) == _lib.WF_ERR_WORKSPACE
+    assert lib.wf_probe_gather_sink_bytes(1, 8, 64) == 8 * 4 * 256 * 4   # 8 pairs x 4 workgroups of 16 rows

@@ -158,20 +158,37 @@ def test_routing_fp16_retriever_cast(device, monkeypatch):
     assert torch.equal(rec[0]["idx"], ref)
 
 
-def test_multiscale_router_merge(device):
-    """MultiScaleRouter.retrieve_indices: both routers' causal top-K on the HIP kernel, then
-    the ascending distinct merge of reference router.py:190-204."""
-    from routing_attention.models import MultiScaleRouter
-    from routing_attention.models.router import merge_candidate_sets
+def test_phase_b_address_scoring_topk(device):
+    """Phase-B scoring without a (B, T, T) matrix: retrieval_topk of an address module, of a
+    per-layer book and of a per-head router returns the causal top-K rows of their dense
+    retrieval_scores -- indices and fp32 scores bit-exact to the C oracle's top-K of the
+    same vectors, and the same sets as torch.topk over the dense scores (rows t >= K-1,
+    near-ties aside) (reference learned_address.py:53-56, router.py:105-115)."""
+    from routing_attention.models import LearnedAddressModule, PerLayerAddressBook
 
-    _say("[models] multi-scale router merge")
-    torch.manual_seed(81)
-    r = MultiScaleRouter(64, routing_dim=16).to(device)
-    x = torch.randn(2, 300, 64, device=device)
-    with torch.no_grad():
-        got = r.retrieve_indices(x, 16)
-        ql, kl = r.local_router.forward_query_key(x)
-        qg, kg = r.global_router.forward_query_key(x)
-    a = native.causal_topk(ql.cpu(), kl.cpu(), 8)
-    b = native.causal_topk(qg.cpu(), kg.cpu(), 8)
-    assert torch.equal(got.cpu(), merge_candidate_sets(a, b, 16))
+    _say("[models] phase-B address scoring on the streaming top-K")
+    torch.manual_seed(83)
+    B, T, K = 2, 700, 64
+    hidden = torch.randn(B, T, 96, generator=torch.Generator().manual_seed(84)).to(device)
+    tri = torch.triu(torch.ones(T, T, dtype=torch.bool, device=device), 1)
+    for name, mod, topk_fn in [
+        ("address", LearnedAddressModule(96, 32).to(device), None),
+        ("book", PerLayerAddressBook(2, 96, 32).to(device), 1),
+        ("router", RouterMLP(96, 16, similarity="asymmetric", n_heads=2, per_head_routing=True).to(device), None),
+    ]:
+        with torch.no_grad():
+            if topk_fn is None:
+                idx, sc = mod.retrieval_topk(hidden, K)
+                q, k = mod.forward_query_key(hidden)
+                dense = mod.retrieval_scores(hidden)
+            else:
+                idx, sc = mod.retrieval_topk(hidden, topk_fn, K)
+                q, k = mod.get_address(topk_fn).forward_query_key(hidden)
+                dense = mod.retrieval_scores(hidden, topk_fn)
+        h = q.shape[2] if q.dim() == 4 else 1
+        ri, rs = native.causal_topk(q.flatten(2).cpu(), k.flatten(2).cpu(), K, return_scores=True)
+        assert torch.equal(idx.cpu(), ri), name
+        assert torch.equal(sc.cpu(), rs / h if h > 1 else rs), name
+        d = torch.topk(dense.masked_fill(tri, float("-inf")), K, dim=-1).indices.sort(-1).values
+        same = (d.cpu() == idx.long().cpu().sort(-1).values).all(-1)[:, K - 1:]
+        assert same.float().mean() > 0.99, name

@@ -105,3 +105,74 @@ def test_readout_int64_indices_and_empty(device):
     z = sparse_meat_attention(q.to(device), k.to(device), v.to(device),
                               torch.zeros(B, T, 0, dtype=torch.int32, device=device), 0.3)
     assert torch.count_nonzero(z) == 0
+
+
+def _lse2_reference(q, k, idx, scale):
+    """Base-2 log-sum-exp of every (b, h, t) row in float64: log2(sum_s exp(scale q.k_s))."""
+    B, H, T, D = q.shape
+    j = idx.long()
+    j = torch.where(j < 0, j + T, j).clamp(0, T - 1)
+    ks = k.double()[torch.arange(B).view(B, 1, 1, 1), torch.arange(H).view(1, H, 1, 1), j.unsqueeze(1)]
+    sc = (q.double().unsqueeze(-2) * ks).sum(-1) * scale
+    return torch.logsumexp(sc, dim=-1) / torch.log(torch.tensor(2.0, dtype=torch.float64))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_readout_generic_kernel_strided_indices(device, dtype):
+    """Index rows with element stride 2 leave the aligned fast kernel: the generic kernel
+    reads every index through its strides. Output and the training forward's lse2."""
+    from routing_attention.kernels.sparse_autograd import readout_fwd_lse
+
+    _say(f"[readout] generic kernel, index stride 2, {dtype}")
+    B, H, T, D, K = 2, 3, 333, 64, 48
+    q, k, v = qkv(B, H, T, D, seed=21, dtype=dtype)
+    g = torch.Generator().manual_seed(22)
+    wide = torch.randint(-T, T, (B, T, 2 * K), generator=g, dtype=torch.int32)
+    idx_dev = wide.to(device)[..., ::2]
+    assert idx_dev.stride(-1) == 2
+    idx = wide[..., ::2].contiguous()
+    scale = D ** -0.5
+    got = sparse_meat_attention(q.to(device), k.to(device), v.to(device), idx_dev, scale)
+    ref = native.sparse_readout(q, k, v, idx, scale)
+    assert rel_err(got.float(), ref) < TOL[dtype]
+    out, lse2 = readout_fwd_lse(q.to(device), k.to(device), v.to(device), idx_dev, scale)
+    assert rel_err(out.float(), ref) < TOL[dtype]
+    lref = _lse2_reference(q, k, idx, scale)
+    assert (lse2.cpu().double() - lref).abs().max().item() < (1e-4 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 32), (torch.float32, 128)])
+def test_readout_generic_kernel_unaligned_qkv(device, dtype, D):
+    """q/k/v views starting one element into their storage: rows are not 16-byte aligned, so
+    the generic kernel's element loads run (VEC off), output into an unaligned view too."""
+    from routing_attention.kernels.sparse_autograd import readout_fwd_lse
+
+    _say(f"[readout] generic kernel, odd element offset, {dtype} D={D}")
+    B, H, T, K = 1, 2, 257, 33
+    n = B * H * T * D
+    g = torch.Generator().manual_seed(23)
+    stores = [torch.randn(n + 1, generator=g).to(dtype) for _ in range(3)]
+    q, k, v = (s[1:].view(B, H, T, D) for s in stores)
+    qa, ka = addresses(B, T, 32, seed=24)
+    idx = native.causal_topk(qa, ka, K)
+    dq, dk, dv = (s.to(device)[1:].view(B, H, T, D) for s in stores)
+    assert dq.data_ptr() % 16 != 0
+    out_store = torch.empty(n + 1, dtype=dtype, device=device)
+    out = out_store[1:].view(B, H, T, D)
+    idx_dev = idx.to(device)
+    scale = 0.17
+    from routing_attention.kernels import _lib
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.wf_sparse_readout_fwd(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _lib.dtype_code(dq),
+                                       B, H, T, D, _lib.strides(dq), _lib.strides(dk), _lib.strides(dv),
+                                       idx_dev.data_ptr(), _lib.strides(idx_dev), K, scale, 0,
+                                       out.data_ptr(), _lib.strides(out), _lib.stream_ptr(device))
+    _lib.check(rc)
+    torch.cuda.synchronize()
+    ref = native.sparse_readout(q, k, v, idx, scale)
+    assert rel_err(out.float(), ref) < TOL[dtype]
+    out2, lse2 = readout_fwd_lse(dq, dk, dv, idx_dev, scale)
+    assert rel_err(out2.float(), ref) < TOL[dtype]
+    lref = _lse2_reference(q, k, idx, scale)
+    assert (lse2.cpu().double() - lref).abs().max().item() < (1e-4 if dtype == torch.float32 else 1e-2)

@@ -1,10 +1,10 @@
 """GPU checks of Recall@K on the streaming top-K (routing_attention/evaluation/recall.py)
-against the reference's dense formulation (recall.py:90-141, 178-235) restated here:
-predicted sets from the C oracle, metrics recomputed with the reference's formulas.
+against the reference's dense formulation (recall.py:89-141) restated here: predicted sets
+from the C oracle, metrics recomputed with the reference's broadcast-compare formulas.
 
 The ground-truth sets are torch.topk of the causal-masked attention on the GPU, as in the
 reference; on rows t < k-1 they include zero-weight future columns chosen by torch's tie
-handling, so the tests take the true sets from the same GPU call the function makes."""
+handling, so the tests take the true sets from the same GPU computation."""
 
 from __future__ import annotations
 
@@ -33,26 +33,31 @@ def _attention(B, T, seed):
 
 
 def _ref_metrics(true_topk, pred_topk, attn_masked, k_eff):
-    # reference recall.py:90-107 restated
+    # reference recall.py:89-107 restated (broadcast comparison of the two index sets)
     th = (true_topk.unsqueeze(-1) == pred_topk.unsqueeze(-2)).any(-1).float()
     ph = (pred_topk.unsqueeze(-1) == true_topk.unsqueeze(-2)).any(-1).float()
     valid = attn_masked.sum(-1) > 0
     return (th.sum(-1) / k_eff)[valid].mean().item(), (ph.sum(-1) / k_eff)[valid].mean().item()
 
 
-def test_recall_from_vectors_matches_reference_formula(device):
+def _true_sets(attn, k, device):
+    true, mass = R._targets(attn.to(device), k, True)
+    am = attn * torch.tril(torch.ones(attn.shape[-1], attn.shape[-1]))
+    return true.cpu(), am
+
+
+def test_recall_from_addresses_matches_reference_formula(device):
     _say("[recall] learned addresses, B2 T512 k32")
     torch.manual_seed(0)
     B, T, k = 2, 512, 32
     mod = LearnedAddressModule(64, 16).to(device)
-    hidden = torch.randn(B, T, 64, generator=torch.Generator().manual_seed(1))
+    hidden = torch.randn(B, T, 64, generator=torch.Generator().manual_seed(1)).to(device)
     attn = _attention(B, T, 2)
-    got = R.compute_recall_from_router(hidden, attn, mod, k=k)
+    got = R.compute_recall_from_addresses(hidden, attn.to(device), mod, k=k)
     with torch.no_grad():
-        qa, ka = mod.forward_query_key(hidden.to(device))
+        qa, ka = mod.forward_query_key(hidden)
     pred = native.causal_topk(qa.cpu(), ka.cpu(), k).long()
-    true, am = R._true_topk(attn.to(device), k)
-    true, am = true.cpu(), am.cpu()
+    true, am = _true_sets(attn, k, device)
     rec, prec = _ref_metrics(true, pred, am, k)
     assert abs(got[f"recall@{k}"] - rec) < 1e-6 and abs(got[f"precision@{k}"] - prec) < 1e-6
     assert got["num_queries"] == B * T
@@ -64,44 +69,36 @@ def test_recall_from_vectors_matches_reference_formula(device):
     assert same.float().mean() > 0.999
 
 
-def test_recall_symmetric_routing_and_by_distance(device):
-    _say("[recall] symmetric routing + by-distance")
+def test_recall_symmetric_routing(device):
+    _say("[recall] symmetric routing vectors")
     B, T, k = 2, 300, 16
     r = torch.nn.functional.normalize(torch.randn(B, T, 24, generator=torch.Generator().manual_seed(3)), dim=-1)
     attn = _attention(B, T, 4)
     got = R.compute_recall_at_k(r.to(device), attn.to(device), k=k)
     pred = native.causal_topk(r, r, k).long()
-    true, am = R._true_topk(attn.to(device), k)
-    true, am = true.cpu(), am.cpu()
-    rec, _ = _ref_metrics(true, pred, am, k)
-    assert abs(got[f"recall@{k}"] - rec) < 1e-6
-    byd = R.compute_recall_by_distance(r.to(device), attn.to(device), k=k)
-    assert abs(byd["overall"][f"recall@{k}"] - rec) < 1e-6
-    dist = (torch.arange(T).view(1, T, 1) - true).abs()
-    in_pred = (true.unsqueeze(-1) == pred.unsqueeze(-2)).any(-1)
-    for b in byd["per_bin"]:
-        sel = (dist > b["distance_min"]) & (dist <= b["distance_max"])
-        assert b["total"] == int(sel.sum()) and b["hits"] == int((sel & in_pred).sum())
+    true, am = _true_sets(attn, k, device)
+    rec, prec = _ref_metrics(true, pred, am, k)
+    assert abs(got[f"recall@{k}"] - rec) < 1e-6 and abs(got[f"precision@{k}"] - prec) < 1e-6
 
 
-def test_recall_per_head_router_and_similarity_path(device):
-    _say("[recall] per-head router (flattened heads) and explicit similarity")
+def test_recall_per_head_router_vectors(device):
+    _say("[recall] per-head router vectors (flattened heads)")
     torch.manual_seed(5)
     B, T, k = 1, 256, 16
     router = RouterMLP(64, 8, similarity="asymmetric", n_heads=4, per_head_routing=True).to(device)
-    hidden = torch.randn(B, T, 64, generator=torch.Generator().manual_seed(6))
+    hidden = torch.randn(B, T, 64, generator=torch.Generator().manual_seed(6)).to(device)
     attn = _attention(B, T, 7)
-    got = R.compute_recall_from_router(hidden, attn, router, k=k)
     with torch.no_grad():
-        q, kk = router.forward_query_key(hidden.to(device))
-        sim = router.retrieval_scores(hidden.to(device))
+        q, kk = router.forward_query_key(hidden)
+        sim = router.retrieval_scores(hidden)
+    got = R.compute_recall_from_vectors(q, kk, attn.to(device), k=k)
     # rows t >= k-1: the head-mean similarity and the flattened dot select the same sets
     # (up to rounding near-ties)
     sim = sim.masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool, device=device), 1), float("-inf"))
     dense = torch.topk(sim, k, dim=-1).indices.sort(-1).values
-    stream = R._pred_topk(q, kk, k).sort(-1).values
+    stream = R._predicted(q, kk, k, True).long().sort(-1).values
     assert (dense == stream).all(-1)[:, k - 1:].float().mean() > 0.99
     pred = native.causal_topk(q.reshape(B, T, -1).cpu(), kk.reshape(B, T, -1).cpu(), k).long()
-    true, am = R._true_topk(attn.to(device), k)
-    rec, _ = _ref_metrics(true.cpu(), pred, am.cpu(), k)
+    true, am = _true_sets(attn, k, device)
+    rec, _ = _ref_metrics(true, pred, am, k)
     assert abs(got[f"recall@{k}"] - rec) < 1e-6

@@ -92,21 +92,25 @@ def test_topk_sliding_window(device):
         assert idx[0, t, :n].tolist() == list(range(t, t - n, -1))
 
 
-def test_topk_all_ties(device):
-    _say("[topk] all ties")
-    B, T, R, K = 1, 900, 32, 128
+@pytest.mark.parametrize("K,T", [(128, 900), (256, 1500), (200, 1200)])
+def test_topk_all_ties(device, K, T):
+    """Every score equal: the lower-index rule selects keys 0..K-1 in every full row (the
+    pools never shrink, so the exact path runs in the loop)."""
+    _say(f"[topk] all ties K={K} T={T}")
+    B, R = 1, 32
     qa = torch.ones(B, T, R, dtype=torch.bfloat16)
     ka = torch.full((B, T, R), 0.25, dtype=torch.bfloat16)
     idx, _ = _check_exact(qa, ka, K, device)
     assert idx[0, -1].tolist() == list(range(K))
 
 
-@pytest.mark.parametrize("K,T", [(128, 3000), (100, 2500)])
+@pytest.mark.parametrize("K,T", [(128, 3000), (100, 2500), (256, 3000), (200, 2600)])
 def test_topk_quantized_score_ties(device, K, T):
     """Addresses in {-1, 0, 1}: every score is a small integer, so each row's K-th place
     falls inside a large group of equal scores and the lower-index rule decides the set.
     Covers the final selection fused into the sort (64 < K <= 128, pools of K..K+16
-    entries) and the radix select alike."""
+    entries), the radix select with 20 and 32 entries per lane (K in (128, 256]) and the
+    in-loop exact path that runs when ties keep a pool from shrinking."""
     _say(f"[topk] quantized ties K={K} T={T}")
     g = torch.Generator().manual_seed(4242 + K)
     B, R = 2, 32

@@ -1,7 +1,7 @@
 """Host-side checks of the model layer that need no GPU: reference names, constructor
-defaults and state_dict keys of the sparse modules, the decoder and the routers; the
-vectorised candidate merge against the reference's per-row loop; the decoder oracle's
-teacher forcing; out-of-scope options raising."""
+defaults and state_dict keys of the sparse modules, the decoder and the router; the
+decoder's loss and capture options; the decoder oracle's teacher forcing; out-of-scope
+options raising."""
 
 from __future__ import annotations
 
@@ -13,16 +13,12 @@ import torch
 from routing_attention.models import (
     KeyVectorSparseAttention,
     LearnedAddressSparseAttention,
-    MultiScaleRouter,
     PerLayerAddressBook,
-    PerLayerRouter,
     RouterMLP,
     RoutingSparseAttention,
     TransformerLM,
     build_address_book_from_config,
-    build_router_from_config,
 )
-from routing_attention.models.router import merge_candidate_sets
 
 
 def _keys(m):
@@ -45,18 +41,23 @@ def test_sparse_module_state_dict_keys():
     assert rs == sorted(proj + [f"router.net.{i}.{p}" for i in (0, 3) for p in ("weight", "bias")])
 
 
-def test_router_config_factory():
-    cfg = {"model": {"d_model": 64, "n_layers": 3, "n_heads": 4}, "router": {}}
-    r = build_router_from_config(cfg)
-    assert isinstance(r, PerLayerRouter) and len(r.routers) == 3
-    cfg["router"] = {"mode": "single", "loss_type": "mse", "routing_dim": 16}
-    r = build_router_from_config(cfg)
-    assert isinstance(r, RouterMLP) and not r.normalize and r.use_affine_dot
-    cfg["router"] = {"mode": "multi_scale"}
-    assert isinstance(build_router_from_config(cfg), MultiScaleRouter)
+def test_address_book_config_and_router_modes():
     book = build_address_book_from_config({"model": {"d_model": 64, "n_layers": 2},
                                            "learned_address": {"address_dim": 16}})
     assert isinstance(book, PerLayerAddressBook) and book.get_address(1).address_dim == 16
+    assert book.get_router(0) is book.get_address(0)
+    alias = build_address_book_from_config({"model": {"d_model": 64, "n_layers": 1},
+                                            "learned_address": {"routing_dim": 8, "similarity": "symmetric"}})
+    assert alias.get_address(0).address_dim == 8 and alias.get_address(0).k_addr_proj is None
+    # a config asking for the reference's per-layer / multi-scale routers raises; single works
+    cfg = {"model": {"d_model": 64, "n_layers": 2}, "router": {}}
+    with pytest.raises(NotImplementedError):
+        TransformerLM(16, 64, 2, 4, 64, 16, attention_type="routing", config=cfg)
+    cfg["router"] = {"mode": "single", "routing_dim": 16, "similarity": "asymmetric"}
+    m = TransformerLM(16, 64, 2, 4, 64, 16, attention_type="routing", config=cfg)
+    assert isinstance(m.router, RouterMLP) and m.blocks[1].attn.router is m.router
+    assert m.router.routing_dim == 16 and hasattr(m.router, "key_net")
+    assert any(k.startswith("router.net.") for k in m.state_dict())
 
 
 def test_router_forward_shapes_and_normalisation():
@@ -73,26 +74,39 @@ def test_router_forward_shapes_and_normalisation():
     torch.testing.assert_close(p, torch.einsum("bthq,bshq->bhts", q, k).mean(dim=2))
 
 
-def _merge_loop(a, b, k):
-    # the per-row loop of reference router.py:195-204, restated
-    B, T, _ = a.shape
-    out = torch.zeros(B, T, k, dtype=torch.long)
-    for bb in range(B):
-        for i in range(T):
-            cand = torch.cat([a[bb, i], b[bb, i]]).unique()
-            n = min(k, cand.numel())
-            out[bb, i, :n] = cand[:n]
-            if n < k:
-                out[bb, i, n:] = cand[0]
-    return out
+def test_router_affine_and_symmetric():
+    torch.manual_seed(1)
+    x = torch.randn(2, 12, 32)
+    r = RouterMLP(32, 8, normalize=False, use_affine_dot=True)
+    q, k = r.forward_query_key(x)
+    assert q is k and q.shape == (2, 12, 8)
+    with torch.no_grad():
+        r.dot_scale.fill_(2.0)
+        r.dot_bias.fill_(-1.0)
+    torch.testing.assert_close(r.pairwise_scores(q), 2.0 * (q @ q.transpose(1, 2)) - 1.0)
+    assert sorted(r.state_dict()) == sorted(["dot_bias", "dot_scale", "net.0.bias", "net.0.weight",
+                                             "net.3.bias", "net.3.weight"])
 
 
-@pytest.mark.parametrize("ka,kb,k,hi", [(4, 4, 8, 6), (4, 4, 8, 50), (3, 5, 8, 4), (1, 1, 2, 3), (8, 8, 10, 9)])
-def test_merge_candidate_sets_matches_reference_loop(ka, kb, k, hi):
-    g = torch.Generator().manual_seed(ka * 100 + kb * 10 + hi)
-    a = torch.randint(0, hi, (2, 7, ka), generator=g)
-    b = torch.randint(0, hi, (2, 7, kb), generator=g)
-    assert torch.equal(merge_candidate_sets(a, b, k), _merge_loop(a, b, k))
+def test_decoder_loss_and_capture_options():
+    """The masked next-token loss equals the per-token cross-entropy averaged over the
+    unmasked targets; hidden states / pre-attention captures and stop_after_layer."""
+    torch.manual_seed(2)
+    m = TransformerLM(20, 32, 3, 2, 64, 16, dropout=0.0, attention_type="dense").eval()
+    ids = torch.randint(1, 20, (2, 16))
+    ids[1, 10:] = 0   # padding (pad_token_id 0) in the second sequence
+    out = m(ids, return_hidden_states=True, return_pre_attention_hidden=True)
+    logits = out["logits"]
+    ce = torch.nn.functional.cross_entropy(logits[:, :-1].reshape(-1, 20), ids[:, 1:].reshape(-1),
+                                           reduction="none").view(2, 15)
+    w = (ids[:, 1:] != 0).float()
+    torch.testing.assert_close(out["loss"], (ce * w).sum() / w.sum())
+    assert len(out["hidden_states"]) == 3 and len(out["pre_attention_hidden"]) == 3
+    torch.testing.assert_close(out["pre_attention_hidden"][1], m.blocks[1].ln1(out["hidden_states"][0]))
+    short = m(ids, return_hidden_states=True, stop_after_layer=0)
+    assert len(short["hidden_states"]) == 1
+    only = m(ids, return_pre_attention_hidden=True, target_layer=2)
+    assert len(only["pre_attention_hidden"]) == 1
 
 
 def test_decoder_signature_and_scope():
@@ -122,6 +136,7 @@ def test_decoder_state_dict_and_tying():
     assert m.blocks[1].attn.address is m.address_book.get_address(1)
     r = TransformerLM(128, 64, 2, 4, 256, 32, attention_type="routing")
     assert r.blocks[0].attn.router is r.blocks[1].attn.router     # one shared RouterMLP
+    assert r.router is None and not any(k.startswith("router.") for k in r.state_dict())
 
 
 def test_decoder_oracle_teacher_forcing_and_self_indices():

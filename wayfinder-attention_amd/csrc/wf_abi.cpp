@@ -7,11 +7,41 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
 
 #include "wf_internal.h"
+
+namespace wf {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+}  // namespace
+
+int device_cu_count()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;   // MI355X; only the dispatch order depends on it
+    g_cu_count[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+int64_t resident_workgroups(const void* kernel, int block)
+{
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    return int64_t(per_cu) * device_cu_count();
+}
+
+}  // namespace wf
 
 namespace {
 
@@ -121,6 +151,7 @@ bool topk_prepare(const void* query, const void* key, int dtype, int64_t B, int6
     p.n_row_blocks = cdiv(T, 16);
     p.rb_begin = 0;
     p.rb_end = p.n_row_blocks;
+    p.n_cus = wf::device_cu_count();
     // vector loads; key rows are addressed with 32-bit byte offsets from the batch base and
     // every 32-dim chunk the kernel reads lies inside the row (R = 32, 64 or 128)
     return (R == 32 || R == 64 || R == 128) &&
@@ -165,7 +196,7 @@ bool readout_rows(wf::ReadoutParams& p, int64_t r0, int64_t r1)
     p.rows_per_seg = cdiv(r1 - r0, p.seg_per_pair);
     p.vpairs = nbh * p.seg_per_pair;
     p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
-    p.head_major = p.vpairs * p.wg_per_vpair > wf::kReadoutResidentWGs ? 1 : 0;
+    p.head_major = 0;   // the launcher decides from the kernel's occupancy
     return p.vpairs * p.wg_per_vpair < (int64_t(1) << 31);
 }
 
@@ -210,6 +241,49 @@ int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t 
         return fail(WF_ERR_UNSUPPORTED, "sparse_readout: problem too large for one launch");
     const hipError_t e = wf::launch_sparse_readout(dtype, vec, fast, p, stream);
     if (e != hipSuccess) return hip_fail("sparse_readout: kernel launch", e);
+    return WF_OK;
+}
+
+// Validation and launches of the fused forward with the workspace `ws` (the caller's, or
+// the library's own scratch for the entry point that allocates nothing).
+int fused_run(const wf_fused_args* a, void* ws, size_t ws_bytes, hipStream_t s)
+{
+    if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "fused: NULL argument struct");
+    int rc = check_topk(a->q_search, a->k_search, a->search_dtype, a->B, a->T, a->R,
+                        a->qs_strides, a->ks_strides, a->top_k, a->out_idx);
+    if (rc != WF_OK) return rc;
+    const int64_t B = a->B, T = a->T, H = a->H;
+    const int64_t k_eff = std::min(a->top_k, T);
+    if (k_eff < 1 && B * T > 0)
+        return fail(WF_ERR_INVALID_ARGUMENT, "fused: top_k must be >= 1 (empty selections have no readout)");
+    const int64_t is[3] = {T * k_eff, k_eff, 1};
+    rc = check_readout(a->q, a->k, a->v, a->dtype, B, H, T, a->D, a->q_strides,
+                       a->k_strides, a->v_strides, a->out_idx, is, k_eff > 0 ? k_eff : 1, a->out,
+                       a->out_strides);
+    if (rc != WF_OK) return rc;
+    if (B * T == 0) return WF_OK;
+    rc = check_topk_ws(B, T, a->R, a->top_k, ws, ws_bytes);
+    if (rc != WF_OK) return rc;
+
+    wf::TopkParams tp;
+    const bool tvec = topk_prepare(a->q_search, a->k_search, a->search_dtype, B, T, a->R, a->qs_strides,
+                                   a->ks_strides, k_eff, a->out_idx, a->out_scores, ws, tp);
+    // the readout's indices are written by the retrieval just before: all in [0, T)
+    wf::ReadoutParams rp;
+    bool rvec = false, rfast = false;
+    if (H > 0 && !readout_prepare(a->q, a->k, a->v, a->dtype, B, H, T, a->D, a->q_strides, a->k_strides,
+                                  a->v_strides, a->out_idx, is, k_eff, a->scale,
+                                  (a->flags & WF_FLAG_MASK_PADS) | wf::kFlagTrustedIndices, a->out,
+                                  a->out_strides, nullptr, rp, &rvec, &rfast))
+        return fail(WF_ERR_UNSUPPORTED, "fused: problem too large for one launch");
+
+    hipError_t e = wf::launch_key_absmax(a->search_dtype, tvec, tp, s);
+    if (e != hipSuccess) return hip_fail("fused: key magnitude kernel launch", e);
+    e = wf::launch_causal_topk(a->search_dtype, tvec, tp, s);
+    if (e != hipSuccess) return hip_fail("fused: retrieval kernel launch", e);
+    if (H == 0) return WF_OK;   // no heads: the indices are still the result's second half
+    e = wf::launch_sparse_readout(a->dtype, rvec, rfast, rp, s);
+    if (e != hipSuccess) return hip_fail("fused: readout kernel launch", e);
     return WF_OK;
 }
 
@@ -378,45 +452,54 @@ int wf_address_project_fwd(const void* x, int dtype, int64_t B, int64_t T, int64
     return ok();
 }
 
+size_t wf_probe_gather_sink_bytes(int64_t B, int64_t H, int64_t T)
+{
+    if (B <= 0 || H <= 0 || T <= 0) return 0;
+    wf::ReadoutParams p{};
+    p.B = B; p.H = H; p.T = T;
+    if (!readout_rows(p, 0, T)) return 0;
+    return size_t(8 * (p.vpairs / 8) * p.wg_per_vpair) * 256u * sizeof(uint32_t);
+}
+
+int wf_probe_gather(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t T,
+                    int64_t D, const int64_t* k_strides, const int64_t* v_strides,
+                    const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                    uint32_t* sink, size_t sink_bytes, void* stream)
+{
+    if (dtype != WF_DTYPE_BF16 && dtype != WF_DTYPE_F16)
+        return fail(WF_ERR_UNSUPPORTED, "probe_gather: 16-bit types only");
+    if (B < 1 || H < 1 || T < 1 || (D != 32 && D != 64 && D != 128))
+        return fail(WF_ERR_INVALID_ARGUMENT, "probe_gather: bad shape");
+    if (K < 4 || K % 4 != 0 || K > kMaxReadoutK)
+        return fail(WF_ERR_UNSUPPORTED, "probe_gather: K must be a multiple of 4 in [4, %lld]", (long long)kMaxReadoutK);
+    if (!k || !v || !indices || !sink || !k_strides || !v_strides || !idx_strides)
+        return fail(WF_ERR_INVALID_ARGUMENT, "probe_gather: NULL pointer");
+    const int64_t es = 2;
+    auto span_ok = [&](const int64_t* st) {
+        return st[2] >= 0 && (T - 1) * st[2] * es + D * es < (int64_t(1) << 32) && st[2] * es < (int64_t(1) << 24);
+    };
+    if (!vec_ok(k, dtype, k_strides, 4, D) || !vec_ok(v, dtype, v_strides, 4, D) || !span_ok(k_strides) ||
+        !span_ok(v_strides) || T > (int64_t(1) << 24) || idx_strides[2] != 1 ||
+        reinterpret_cast<uintptr_t>(indices) % 16 != 0 || idx_strides[0] % 4 != 0 || idx_strides[1] % 4 != 0)
+        return fail(WF_ERR_UNSUPPORTED, "probe_gather: needs the readout's fast layout");
+    if (sink_bytes < wf_probe_gather_sink_bytes(B, H, T))
+        return fail(WF_ERR_WORKSPACE, "probe_gather: sink of %zu bytes required", wf_probe_gather_sink_bytes(B, H, T));
+    wf::ReadoutParams p{};
+    p.k = k; p.v = v; p.idx = indices;
+    for (int i = 0; i < 4; ++i) { p.ks[i] = k_strides[i]; p.vs[i] = v_strides[i]; }
+    for (int i = 0; i < 3; ++i) p.is[i] = idx_strides[i];
+    p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
+    if (!readout_rows(p, 0, T)) return fail(WF_ERR_UNSUPPORTED, "probe_gather: problem too large");
+    const hipError_t e = wf::launch_gather_probe(dtype, p, sink, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("probe_gather: kernel launch", e);
+    return ok();
+}
+
 int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
 {
-    if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "fused: NULL argument struct");
-    int rc = check_topk(a->q_search, a->k_search, a->search_dtype, a->B, a->T, a->R,
-                        a->qs_strides, a->ks_strides, a->top_k, a->out_idx);
-    if (rc != WF_OK) return rc;
-    const int64_t B = a->B, T = a->T;
-    const int64_t k_eff = std::min(a->top_k, T);
-    if (k_eff < 1 && B * T > 0)
-        return fail(WF_ERR_INVALID_ARGUMENT, "fused: top_k must be >= 1 (empty selections have no readout)");
-    const int64_t is[3] = {T * k_eff, k_eff, 1};
-    rc = check_readout(a->q, a->k, a->v, a->dtype, B, a->H, T, a->D, a->q_strides,
-                       a->k_strides, a->v_strides, a->out_idx, is, k_eff > 0 ? k_eff : 1, a->out,
-                       a->out_strides);
-    if (rc != WF_OK) return rc;
-    if (B * T == 0 || a->H == 0) return ok();
-    rc = check_topk_ws(B, T, a->R, a->top_k, a->workspace, a->workspace_bytes);
-    if (rc != WF_OK) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-
-    wf::TopkParams tp;
-    const bool tvec = topk_prepare(a->q_search, a->k_search, a->search_dtype, B, T, a->R, a->qs_strides,
-                                   a->ks_strides, k_eff, a->out_idx, a->out_scores, a->workspace, tp);
-    // the readout's indices are written by the retrieval just before: all in [0, T)
-    wf::ReadoutParams rp;
-    bool rvec, rfast;
-    if (!readout_prepare(a->q, a->k, a->v, a->dtype, B, a->H, T, a->D, a->q_strides, a->k_strides,
-                         a->v_strides, a->out_idx, is, k_eff, a->scale,
-                         (a->flags & WF_FLAG_MASK_PADS) | wf::kFlagTrustedIndices, a->out,
-                         a->out_strides, nullptr, rp, &rvec, &rfast))
-        return fail(WF_ERR_UNSUPPORTED, "fused: problem too large for one launch");
-
-    hipError_t e = wf::launch_key_absmax(a->search_dtype, tvec, tp, s);
-    if (e != hipSuccess) return hip_fail("fused: key magnitude kernel launch", e);
-    e = wf::launch_causal_topk(a->search_dtype, tvec, tp, s);
-    if (e != hipSuccess) return hip_fail("fused: retrieval kernel launch", e);
-    e = wf::launch_sparse_readout(a->dtype, rvec, rfast, rp, s);
-    if (e != hipSuccess) return hip_fail("fused: readout kernel launch", e);
-    return ok();
+    const int rc = fused_run(a, a ? a->workspace : nullptr, a ? a->workspace_bytes : 0,
+                             static_cast<hipStream_t>(stream));
+    return rc == WF_OK ? ok() : rc;
 }
 
 }  // extern "C"

@@ -108,6 +108,7 @@ struct TopkParams {
     int64_t n_chunks;
     int64_t n_row_blocks;    // ceil(T / 16)
     int64_t rb_begin, rb_end;  // row blocks [rb_begin, rb_end) of this launch
+    int64_t n_cus;           // compute units of the device (dispatch order of the row blocks)
 };
 
 struct ReadoutParams {
@@ -129,7 +130,8 @@ struct ReadoutParams {
     int64_t vpairs;         // B*H*seg_per_pair virtual pairs
     int64_t wg_per_vpair;   // workgroups per virtual pair
     int head_major;         // workgroup order: 1 = virtual pair by virtual pair (grids larger
-                            // than one residency wave), 0 = pair blockIdx % 8 (one wave)
+                            // than one residency wave), 0 = pair blockIdx % 8 (one wave);
+                            // set by the launcher from the kernel's occupancy
 };
 
 // Backward of the readout (fixed indices). Both passes pair blockIdx % 8 with a fixed set of
@@ -183,13 +185,13 @@ constexpr unsigned kFlagTrustedIndices = 0x80000000u;
 constexpr int kAbsmaxChunk = 256;
 // Query rows per readout workgroup (4 waves x 4 consecutive rows).
 constexpr int kReadoutRowsPerWG = 16;
-// Readout workgroups resident at once on MI355X (256 CUs x 5 workgroups of 4 waves at the
-// fast kernel's 5 waves per SIMD): grids above this run in several residency waves.
-constexpr int64_t kReadoutResidentWGs = 1280;
+// Compute units of the current device, read once per device (hipDeviceGetAttribute) and
+// cached; thread-safe. Only scheduling decisions depend on it, never results.
+int device_cu_count();
 
-// Retrieval workgroups that fill one slot of every CU on MI355X (256 CUs, two retrieval
-// workgroups per CU): in the first residency wave workgroups c and c + 256 share a CU.
-constexpr int64_t kTopkCUs = 256;
+// Workgroups of `kernel` (block of `block` threads, no dynamic LDS) resident at once on the
+// current device: CUs x the kernel's occupancy per CU. The caller caches it per device.
+int64_t resident_workgroups(const void* kernel, int block);
 
 // launchers (return hipError_t of the launch)
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
@@ -200,5 +202,7 @@ hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutPa
 size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K);
 hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_address_project(int dtype, const AddressParams& p, hipStream_t s);
+// measurement aid (wf_probe.hip): the readout's gathers without its arithmetic, 16-bit types
+hipError_t launch_gather_probe(int dtype, const ReadoutParams& p, uint32_t* sink, hipStream_t s);
 
 }  // namespace wf

@@ -16,6 +16,8 @@
 //    bytes, 4 MiB at the benchmark shape, one XCD's L2): pair by pair for grids that run in
 //    several residency waves, blockIdx % 8 -> fixed pairs (one XCD each under the initial
 //    round-robin dispatch) for grids that fit in one (readout_block).
+#include <atomic>
+
 #include "wf_readout_dev.h"
 
 namespace wf {
@@ -396,6 +398,34 @@ void sparse_readout_fast(ReadoutParams p)
     }
 }
 
+// Workgroups of KFN resident at once on the current device, computed once per device from
+// the kernel's occupancy and cached (one cache per kernel instantiation).
+template <void (*KFN)(ReadoutParams)>
+int64_t resident_cached()
+{
+    static std::atomic<int64_t> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return resident_workgroups(reinterpret_cast<const void*>(KFN), 64 * kWaves);
+    int64_t n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        n = resident_workgroups(reinterpret_cast<const void*>(KFN), 64 * kWaves);
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Launch KFN over the grid of p. A grid larger than one residency wave runs virtual pair by
+// virtual pair (head_major), a smaller one pairs blockIdx % 8 with fixed pairs.
+template <void (*KFN)(ReadoutParams)>
+hipError_t launch_readout(ReadoutParams p, hipStream_t s)
+{
+    const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
+    p.head_major = grid > resident_cached<KFN>() ? 1 : 0;
+    KFN<<<dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), 0, s>>>(p);
+    return hipGetLastError();
+}
+
 template <typename DT, int D>
 hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
 {
@@ -403,22 +433,18 @@ hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
 #define WF_READOUT_FAST_NB 4
 #endif
     constexpr int NB = WF_READOUT_FAST_NB;
-    const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
-    const dim3 g(static_cast<unsigned>(grid)), blk(64 * kWaves);
     // 16-byte index loads: K a multiple of 4 (row starts stay 16-byte aligned given an
     // aligned base and row strides that are multiples of 4)
     const bool vi = NB == 4 && p.K % 4 == 0 && p.K >= NB && reinterpret_cast<uintptr_t>(p.idx) % 16 == 0 &&
                     p.is[0] % 4 == 0 && p.is[1] % 4 == 0;
     if (vi) {
-        if (p.lse2) sparse_readout_fast<DT, D, NB, true, false, true><<<g, blk, 0, s>>>(p);
-        else if (p.flags & kFlagTrustedIndices) sparse_readout_fast<DT, D, NB, false, true, true><<<g, blk, 0, s>>>(p);
-        else sparse_readout_fast<DT, D, NB, false, false, true><<<g, blk, 0, s>>>(p);
-    } else {
-        if (p.lse2) sparse_readout_fast<DT, D, NB, true, false, false><<<g, blk, 0, s>>>(p);
-        else if (p.flags & kFlagTrustedIndices) sparse_readout_fast<DT, D, NB, false, true, false><<<g, blk, 0, s>>>(p);
-        else sparse_readout_fast<DT, D, NB, false, false, false><<<g, blk, 0, s>>>(p);
+        if (p.lse2) return launch_readout<sparse_readout_fast<DT, D, NB, true, false, true>>(p, s);
+        if (p.flags & kFlagTrustedIndices) return launch_readout<sparse_readout_fast<DT, D, NB, false, true, true>>(p, s);
+        return launch_readout<sparse_readout_fast<DT, D, NB, false, false, true>>(p, s);
     }
-    return hipGetLastError();
+    if (p.lse2) return launch_readout<sparse_readout_fast<DT, D, NB, true, false, false>>(p, s);
+    if (p.flags & kFlagTrustedIndices) return launch_readout<sparse_readout_fast<DT, D, NB, false, true, false>>(p, s);
+    return launch_readout<sparse_readout_fast<DT, D, NB, false, false, false>>(p, s);
 }
 
 template <typename DT>
@@ -432,13 +458,11 @@ hipError_t launch_fast_t(const ReadoutParams& p, hipStream_t s)
 template <typename DT, bool VEC, int D>
 hipError_t launch_d(const ReadoutParams& p, hipStream_t s)
 {
-    const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
 #ifndef WF_READOUT_NB
 #define WF_READOUT_NB 4
 #endif
     constexpr int NB = WF_READOUT_NB;
-    sparse_readout_kernel<DT, VEC, D, NB><<<dim3(unsigned(grid)), dim3(64 * kWaves), 0, s>>>(p);
-    return hipGetLastError();
+    return launch_readout<sparse_readout_kernel<DT, VEC, D, NB>>(p, s);
 }
 
 template <typename DT, bool VEC>

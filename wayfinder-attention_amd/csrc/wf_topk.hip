@@ -814,12 +814,14 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p)
     const int64_t T = p.T;
     // Workgroups take (batch, row block) pairs longest causal prefix first, except that the
     // second half of the first residency wave runs in reverse: the two workgroups that start
-    // on one CU (c and c + kTopkCUs) then hold positions c and 2 kTopkCUs - 1 - c, whose
-    // prefix lengths sum to the same total on every CU (config 4: 0.157 -> 0.150 ms). Any
-    // order is a permutation of the same blocks, so results do not depend on it.
+    // on one CU (c and c + n_cus, two retrieval workgroups fit a CU) then hold positions c and
+    // 2 n_cus - 1 - c, whose prefix lengths sum to the same total on every CU (config 4:
+    // 0.157 -> 0.150 ms). Any order is a permutation of the same blocks, so results do not
+    // depend on it.
     int64_t pos = blockIdx.x;
-    if (p.B * (p.rb_end - p.rb_begin) >= 2 * kTopkCUs && pos >= kTopkCUs && pos < 2 * kTopkCUs)
-        pos = 3 * kTopkCUs - 1 - pos;
+    const int64_t ncu = p.n_cus;
+    if (p.B * (p.rb_end - p.rb_begin) >= 2 * ncu && pos >= ncu && pos < 2 * ncu)
+        pos = 3 * ncu - 1 - pos;
     const int64_t b = pos % p.B;
     const int64_t rb = p.rb_end - 1 - pos / p.B;
     const int64_t r0 = rb * kRows;

@@ -19,6 +19,10 @@ from routing_attention.kernels._common import has_hip, promote_compute_dtype
 # Method names of the reference (causal_topk.py:480-487, 501-521). All map to the HIP kernel.
 METHODS = ("auto", "fused_causal", "triton", "tiled", "streaming", "brute_force")
 
+# Largest address dim (R) and k_eff the HIP kernel takes (include/wayfinder_hip.h).
+MAX_ADDRESS_DIM = 128
+MAX_TOP_K = 256
+
 
 def causal_topk_available() -> bool:
     """True when the HIP kernels can run (reference causal_topk.py:33-34)."""

@@ -12,12 +12,7 @@ from routing_attention.models.learned_address import (
     PerLayerAddressBook,
     build_address_book_from_config,
 )
-from routing_attention.models.router import (
-    MultiScaleRouter,
-    PerLayerRouter,
-    RouterMLP,
-    build_router_from_config,
-)
+from routing_attention.models.router import RouterMLP
 from routing_attention.models.transformer import TransformerBlock, TransformerLM
 
 __all__ = [
@@ -25,13 +20,10 @@ __all__ = [
     "KeyVectorSparseAttention",
     "LearnedAddressModule",
     "LearnedAddressSparseAttention",
-    "MultiScaleRouter",
     "PerLayerAddressBook",
-    "PerLayerRouter",
     "RouterMLP",
     "RoutingSparseAttention",
     "TransformerBlock",
     "TransformerLM",
     "build_address_book_from_config",
-    "build_router_from_config",
 ]

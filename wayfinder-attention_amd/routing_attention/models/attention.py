@@ -27,7 +27,6 @@ from routing_attention.kernels.fused_sparse import (
 )
 from routing_attention.kernels.sparse_autograd import sparse_readout
 from routing_attention.models.learned_address import LearnedAddressModule
-from routing_attention.models.router import MultiScaleRouter, PerLayerRouter
 from routing_attention.retrieval.index import (
     RetrievalConfig,
     RoutingRetriever,
@@ -291,7 +290,9 @@ class LearnedAddressSparseAttention(nn.Module):
 
 class RoutingSparseAttention(nn.Module):
     """Sparse attention with router vectors for retrieval (reference attention.py:504-617).
-    Supports RouterMLP, PerLayerRouter (via layer_idx) and MultiScaleRouter."""
+    The router is a RouterMLP, a per-layer container (anything with ``get_router``, picked
+    by layer_idx) or a candidate generator of its own (anything with ``retrieve_indices``,
+    the reference's multi-scale router)."""
 
     def __init__(
         self,
@@ -327,17 +328,17 @@ class RoutingSparseAttention(nn.Module):
             )
 
     def _get_query_key_routing(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        # reference :555-563
-        if isinstance(self.router, PerLayerRouter):
-            return self.router.get_router(self.layer_idx).forward_query_key(x)
-        if hasattr(self.router, "forward_query_key"):
-            return self.router.forward_query_key(x)
-        r = self.router(x)
+        """(query, key) routing vectors of this layer (reference :548-555)."""
+        router = self.router.get_router(self.layer_idx) if hasattr(self.router, "get_router") else self.router
+        if hasattr(router, "forward_query_key"):
+            return router.forward_query_key(x)
+        r = router(x)
         return r, r
 
     def _retrieve_candidates(self, x: torch.Tensor) -> torch.Tensor:
-        # reference :565-575
-        if isinstance(self.router, MultiScaleRouter):
+        """(B, T, top_k) neighbours: the router's own candidate generator if it has one,
+        else the causal top-K of its vectors (reference :557-566)."""
+        if hasattr(self.router, "retrieve_indices"):
             return self.router.retrieve_indices(x, self.top_k, self.layer_idx)
         q, k = self._get_query_key_routing(x)
         return self.retriever(q, k, top_k=self.top_k)

@@ -1,12 +1,14 @@
-"""Decoder-only language model around the sparse attention modules (mirrors
-routing_attention/models/transformer.py of the reference: TransformerBlock (:26-73) and
-TransformerLM (:76-401) with the same constructor, submodule names, state_dict keys, weight
-tying and loss).
+"""Decoder-only language model around the sparse attention modules (the reference's
+routing_attention/models/transformer.py: TransformerBlock :26-73 and TransformerLM
+:76-401). Kept from the reference, as interface: the constructor arguments, the submodule
+names and hence the state_dict keys (token_emb, pos_emb, blocks.<i>.{ln1, attn, ln2, ff.0,
+ff.3}, ln_f, lm_head tied to token_emb, digit_head), and the value of the masked
+next-token loss.
 
-Attention types on the MI355X path: ``learned_address``, ``key_vector``, ``routing`` (the
-top-K sparse modules, HIP retrieval + readout) and ``dense`` / ``dense_flash``
-(F.scaled_dot_product_attention, the comparator). ``linear`` and ``local`` attention and
-the pointer / pool output heads are not part of this build and raise.
+Attention types here: ``learned_address``, ``key_vector`` and ``routing`` (the top-K sparse
+modules: HIP retrieval and readout) and ``dense`` / ``dense_flash`` (causal SDPA, the
+comparator). ``linear`` and ``local`` attention, the pointer / pool output heads and the
+per-layer / multi-scale router configurations are outside this build and raise.
 """
 
 from __future__ import annotations
@@ -24,45 +26,53 @@ from routing_attention.models.attention import (
     RoutingSparseAttention,
 )
 from routing_attention.models.learned_address import build_address_book_from_config
-from routing_attention.models.router import RouterMLP, build_router_from_config
-
-_OUT_OF_SCOPE_ATTENTION = ("linear", "local")
+from routing_attention.models.router import RouterMLP
 
 
 class TransformerBlock(nn.Module):
-    """Pre-norm block: x + attn(ln1(x)), then x + ff(ln2(x)) (reference :26-73)."""
+    """Pre-norm residual block: x + attn(ln1 x), then + ff(ln2 .) with a 4-module MLP
+    (Linear, GELU, Dropout, Linear) followed by dropout."""
 
     def __init__(self, d_model: int, n_heads: int, d_ff: int, dropout: float,
                  attention_module: nn.Module, layer_idx: int = 0):
         super().__init__()
-        self.attn = attention_module
+        del n_heads   # carried by the attention module
         self.layer_idx = layer_idx
         self.ln1 = nn.LayerNorm(d_model)
+        self.attn = attention_module
         self.ln2 = nn.LayerNorm(d_model)
-        self.ff = nn.Sequential(
-            nn.Linear(d_model, d_ff),
-            nn.GELU(),
-            nn.Dropout(dropout),
-            nn.Linear(d_ff, d_model),
-            nn.Dropout(dropout),
-        )
+        self.ff = nn.Sequential(nn.Linear(d_model, d_ff), nn.GELU(), nn.Dropout(dropout),
+                                nn.Linear(d_ff, d_model), nn.Dropout(dropout))
 
     def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None,
                 return_attention: bool = False, return_per_head: bool = False, **attn_kwargs):
-        residual = x
-        x_norm = self.ln1(x)
+        """Returns x, or (x, attention weights) with ``return_attention``."""
         if return_attention:
-            attn_out, attn_w = self.attn(x_norm, attn_mask=attn_mask, return_attention=True,
-                                         return_per_head=return_per_head, **attn_kwargs)
-            x = residual + attn_out
-            x = x + self.ff(self.ln2(x))
-            return x, attn_w
-        x = residual + self.attn(x_norm, attn_mask=attn_mask, **attn_kwargs)
-        return x + self.ff(self.ln2(x))
+            attn_kwargs.update(return_attention=True, return_per_head=return_per_head)
+        a = self.attn(self.ln1(x), attn_mask=attn_mask, **attn_kwargs)
+        a, weights = a if return_attention else (a, None)
+        x = x + a
+        x = x + self.ff(self.ln2(x))
+        return (x, weights) if return_attention else x
+
+
+def _router_from_config(d_model: int, config: dict) -> RouterMLP:
+    """The router a config asks for. Only its single-router mode is part of this build
+    (the reference's default, per-layer, and its multi-scale mode are not)."""
+    section = config.get("router") or {}
+    mode = section.get("mode", "per_layer")
+    if mode != "single":
+        raise NotImplementedError(f"router mode {mode!r} is not part of this build; "
+                                  "pass router=RouterMLP(...) instead")
+    return RouterMLP(d_model, section.get("routing_dim", 32), section.get("hidden_dim"),
+                     similarity=section.get("similarity", "symmetric"))
 
 
 class TransformerLM(nn.Module):
-    """Decoder-only transformer for language modelling (reference :76-401)."""
+    """Decoder-only transformer language model (token + learned position embeddings,
+    pre-norm blocks, final LayerNorm, LM head tied to the token embedding)."""
+
+    _SPARSE = ("learned_address", "key_vector", "routing")
 
     def __init__(
         self,
@@ -93,92 +103,95 @@ class TransformerLM(nn.Module):
         del local_window, pointer_mlp_hidden, num_pointer_slots, pool_mlp_positions
         if output_head != "lm_token":
             raise NotImplementedError(f"output_head={output_head!r} is not part of this build")
-        if attention_type in _OUT_OF_SCOPE_ATTENTION:
+        if attention_type in ("linear", "local"):
             raise NotImplementedError(f"attention_type={attention_type!r} is not part of this build")
-        self.d_model = d_model
+        if attention_type not in self._SPARSE + ("dense", "dense_flash"):
+            raise ValueError(f"Unknown attention_type: {attention_type}")
+        self.attention_type = attention_type
+        self.d_model, self.n_layers, self.n_heads = d_model, n_layers, n_heads
+        self.max_seq_len = max_seq_len
+        self.pad_token_id = pad_token_id
+        self.routing_top_k = routing_top_k
         self.output_head = output_head
         self.pointer_target_mode = pointer_target_mode
-        self.max_seq_len = max_seq_len
-        self.n_layers = n_layers
-        self.n_heads = n_heads
-        self.pad_token_id = pad_token_id
-        self.attention_type = attention_type
-        self.routing_top_k = routing_top_k
-        self.retrieval_config = retrieval_config
-        if retrieval_config is None and config is not None:
-            self.retrieval_config = config.get("retrieval")
-        if router is None and attention_type == "routing" and config is not None:
-            router = build_router_from_config(config)
+        self.retrieval_config = retrieval_config if retrieval_config is not None else (config or {}).get("retrieval")
+        if attention_type == "routing" and router is None and config is not None:
+            router = _router_from_config(d_model, config)
         self.router = router
-        self.address_book = None
-        la_cfg = (config or {}).get("learned_address", {})
+        # without a router, the routing layers share one RouterMLP that only the blocks hold
+        # (the model's own `router` stays None, as in the reference)
+        shared = router
+        if attention_type == "routing" and shared is None:
+            shared = RouterMLP(d_model, routing_dim=32)
+        self.address_book = (build_address_book_from_config(config)
+                             if attention_type == "learned_address" and config is not None else None)
 
         self.token_emb = nn.Embedding(vocab_size, d_model)
         self.pos_emb = nn.Embedding(max_seq_len, d_model)
         self.dropout = nn.Dropout(dropout)
-
-        self.blocks = nn.ModuleList()
-        for layer_idx in range(n_layers):
-            if attention_type in ("dense", "dense_flash"):
-                attn = DenseSDPAAttention(d_model, n_heads, dropout)
-            elif attention_type == "key_vector":
-                attn = KeyVectorSparseAttention(d_model, n_heads, routing_top_k, dropout,
-                                                retrieval_config=self.retrieval_config)
-            elif attention_type == "learned_address":
-                if self.address_book is None and config is not None:
-                    self.address_book = build_address_book_from_config(config)
-                addr_mod = (self.address_book.get_address(layer_idx)
-                            if self.address_book is not None else None)
-                attn = LearnedAddressSparseAttention(
-                    d_model, n_heads, routing_top_k,
-                    address_dim=la_cfg.get("address_dim", 32),
-                    similarity=la_cfg.get("similarity", "asymmetric"),
-                    dropout=dropout, address_module=addr_mod,
-                    retrieval_config=self.retrieval_config,
-                )
-            elif attention_type == "routing":
-                if router is None:
-                    router = RouterMLP(d_model, routing_dim=32)
-                attn = RoutingSparseAttention(d_model, n_heads, router, routing_top_k, dropout,
-                                              layer_idx=layer_idx,
-                                              retrieval_config=self.retrieval_config)
-            else:
-                raise ValueError(f"Unknown attention_type: {attention_type}")
-            self.blocks.append(TransformerBlock(d_model, n_heads, d_ff, dropout, attn, layer_idx=layer_idx))
-
+        self.blocks = nn.ModuleList(
+            TransformerBlock(d_model, n_heads, d_ff, dropout,
+                             self._attention(i, d_model, n_heads, dropout, config, shared), layer_idx=i)
+            for i in range(n_layers))
         self.ln_f = nn.LayerNorm(d_model)
         self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
         self.lm_head.weight = self.token_emb.weight
         self.num_digit_classes = num_digit_classes
         self.digit_head = nn.Linear(d_model, num_digit_classes) if num_digit_classes > 0 else None
 
-    def get_router_parameters(self):
-        return [] if self.router is None else list(self.router.parameters())
+    def _attention(self, layer: int, d_model: int, n_heads: int, dropout: float,
+                   config: Optional[dict], router: Optional[nn.Module]) -> nn.Module:
+        kind, k, rc = self.attention_type, self.routing_top_k, self.retrieval_config
+        if kind in ("dense", "dense_flash"):
+            return DenseSDPAAttention(d_model, n_heads, dropout)
+        if kind == "key_vector":
+            return KeyVectorSparseAttention(d_model, n_heads, k, dropout, retrieval_config=rc)
+        if kind == "routing":
+            return RoutingSparseAttention(d_model, n_heads, router, k, dropout, layer_idx=layer,
+                                          retrieval_config=rc)
+        section = (config or {}).get("learned_address") or {}
+        return LearnedAddressSparseAttention(
+            d_model, n_heads, k, address_dim=section.get("address_dim", 32),
+            similarity=section.get("similarity", "asymmetric"), dropout=dropout,
+            address_module=self.address_book.get_address(layer) if self.address_book is not None else None,
+            retrieval_config=rc)
 
-    def get_address_parameters(self):
+    # ---- parameter groups (Phase A / Phase B training freezes one or the other)
+    def get_router_parameters(self) -> list:
+        return list(self.router.parameters()) if self.router is not None else []
+
+    def get_address_parameters(self) -> list:
         if self.address_book is not None:
             return list(self.address_book.parameters())
-        params = []
-        for block in self.blocks:
-            if hasattr(block.attn, "address"):
-                params.extend(block.attn.address.parameters())
-        return params
+        mods = [b.attn.address for b in self.blocks if hasattr(b.attn, "address")]
+        return [p for m in mods for p in m.parameters()]
+
+    @staticmethod
+    def _set_trainable(params, flag: bool) -> None:
+        for p in params:
+            p.requires_grad_(flag)
 
     def freeze_router(self) -> None:
-        for p in self.get_router_parameters():
-            p.requires_grad = False
+        self._set_trainable(self.get_router_parameters(), False)
 
     def unfreeze_router(self) -> None:
-        for p in self.get_router_parameters():
-            p.requires_grad = True
+        self._set_trainable(self.get_router_parameters(), True)
 
     def freeze_addresses(self) -> None:
-        for p in self.get_address_parameters():
-            p.requires_grad = False
+        self._set_trainable(self.get_address_parameters(), False)
 
     def unfreeze_addresses(self) -> None:
-        for p in self.get_address_parameters():
-            p.requires_grad = True
+        self._set_trainable(self.get_address_parameters(), True)
+
+    # ---- forward
+    def _next_token_loss(self, logits: torch.Tensor, input_ids: torch.Tensor,
+                         attn_mask: torch.Tensor) -> torch.Tensor:
+        """Mean cross-entropy of positions 1..T-1 whose mask entry is set."""
+        keep = attn_mask[:, 1:].bool()
+        targets = input_ids[:, 1:].masked_fill(~keep, -100)
+        total = F.cross_entropy(logits[:, :-1].reshape(-1, logits.shape[-1]), targets.reshape(-1),
+                                ignore_index=-100, reduction="sum")
+        return total / keep.sum().clamp(min=1)
 
     def forward(
         self,
@@ -195,55 +208,40 @@ class TransformerLM(nn.Module):
         target_layer: Optional[int] = None,
         stop_after_layer: Optional[int] = None,
     ) -> dict[str, torch.Tensor]:
-        """Token ids (B, T) -> {"logits", "loss", ...} (reference :272-401, lm_token head)."""
+        """Token ids (B, T) -> {"logits", "loss"} plus what the return_* flags ask for.
+        ``target_layer`` restricts attention / pre-attention capture (and the
+        ``stop_after_layer`` check) to that layer."""
         del question_index, pointer_target_index, pointer_target_slot
-        B, T = input_ids.shape
-        if attn_mask is None:
-            attn_mask = input_ids != self.pad_token_id
-        pos = torch.arange(T, device=input_ids.device).unsqueeze(0)
-        x = self.dropout(self.token_emb(input_ids) + self.pos_emb(pos))
-
-        hidden_states, pre_attention_hidden, attentions = [], [], []
-        for layer_idx, block in enumerate(self.blocks):
-            if target_layer is not None and layer_idx != target_layer:
-                x = block(x, attn_mask=attn_mask)
-                if return_hidden_states:
-                    hidden_states.append(x)
-                continue
-            if return_pre_attention_hidden:
-                pre_attention_hidden.append(block.ln1(x))
-            if return_attentions:
-                x, attn_w = block(x, attn_mask=attn_mask, return_attention=True,
-                                  return_per_head=return_per_head_attention)
-                attentions.append(attn_w)
+        T = input_ids.shape[1]
+        mask = attn_mask if attn_mask is not None else input_ids != self.pad_token_id
+        x = self.dropout(self.token_emb(input_ids) + self.pos_emb.weight[:T].unsqueeze(0))
+        caught = {"hidden_states": [], "attentions": [], "pre_attention_hidden": []}
+        for i, block in enumerate(self.blocks):
+            watched = target_layer is None or i == target_layer
+            if watched and return_pre_attention_hidden:
+                caught["pre_attention_hidden"].append(block.ln1(x))
+            if watched and return_attentions:
+                x, w = block(x, attn_mask=mask, return_attention=True,
+                             return_per_head=return_per_head_attention)
+                caught["attentions"].append(w)
             else:
-                x = block(x, attn_mask=attn_mask)
+                x = block(x, attn_mask=mask)
             if return_hidden_states:
-                hidden_states.append(x)
-            if stop_after_layer is not None and layer_idx >= stop_after_layer:
+                caught["hidden_states"].append(x)
+            if watched and stop_after_layer is not None and i >= stop_after_layer:
                 break
-
         x = self.ln_f(x)
         logits = self.lm_head(x)
-        output: dict[str, torch.Tensor] = {"logits": logits}
-
-        # next-token loss over non-pad targets (reference :361-373)
-        shift_logits = logits[:, :-1, :].contiguous()
-        shift_labels = input_ids[:, 1:].contiguous()
-        shift_mask = attn_mask[:, 1:].contiguous().float()
-        loss = F.cross_entropy(shift_logits.view(-1, shift_logits.size(-1)), shift_labels.view(-1),
-                               reduction="none").view(B, T - 1)
-        output["loss"] = (loss * shift_mask).sum() / shift_mask.sum().clamp(min=1)
+        out: dict[str, torch.Tensor] = {"logits": logits,
+                                        "loss": self._next_token_loss(logits, input_ids, mask)}
         if self.digit_head is not None and labels is not None:
-            mask = attn_mask.float()
-            pooled = (x * mask.unsqueeze(-1)).sum(dim=1) / mask.sum(dim=1, keepdim=True).clamp(min=1)
+            w = mask.to(x.dtype).unsqueeze(-1)
+            pooled = (x * w).sum(dim=1) / w.sum(dim=1).clamp(min=1)
             digit_logits = self.digit_head(pooled)
-            output["digit_loss"] = F.cross_entropy(digit_logits, labels)
-            output["digit_accuracy"] = (digit_logits.argmax(dim=-1) == labels).float().mean()
-        if return_hidden_states:
-            output["hidden_states"] = hidden_states
-        if return_pre_attention_hidden:
-            output["pre_attention_hidden"] = pre_attention_hidden
-        if return_attentions:
-            output["attentions"] = attentions
-        return output
+            out["digit_loss"] = F.cross_entropy(digit_logits, labels)
+            out["digit_accuracy"] = (digit_logits.argmax(dim=-1) == labels).float().mean()
+        for flag, name in ((return_hidden_states, "hidden_states"), (return_attentions, "attentions"),
+                           (return_pre_attention_hidden, "pre_attention_hidden")):
+            if flag:
+                out[name] = caught[name]
+        return out
