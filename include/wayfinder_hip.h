@@ -227,6 +227,19 @@ size_t wf_fused_workspace_bytes(int64_t B, int64_t T, int64_t R, int64_t top_k);
 int wf_fused_topk_sparse_fwd(const wf_fused_args* args, void* stream);
 
 /*
+ * wf_fused_topk_sparse_fwd for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. Same arguments, results and errors as wf_fused_topk_sparse_fwd except that
+ * args->workspace / workspace_bytes are ignored: the retrieval's scratch (B * ceil(T / 256)
+ * floats) comes from a 1 MiB array the library keeps on each device until the process ends,
+ * so shapes with B * ceil(T / 256) > 262144 are rejected (WF_ERR_UNSUPPORTED). Calls no
+ * allocating routine. Calls that overlap on one device share that array and race: issue
+ * them on one stream, or serialise them.
+ */
+size_t wf_fused_noalloc_scratch_limit(void);
+int wf_fused_topk_sparse_fwd_noalloc(const wf_fused_args* args, void* stream);
+
+/*
  * Measurement aid, no reference counterpart: the readout's gather path with no arithmetic.
  * Issues exactly the loads of wf_sparse_readout_fwd's fast kernel (same grid, workgroup
  * order, 16-byte index loads and K/V row gathers, two tasks in flight per wave) and folds

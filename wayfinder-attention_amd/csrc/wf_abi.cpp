@@ -10,6 +10,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "wf_internal.h"
@@ -241,6 +242,39 @@ int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t 
         return fail(WF_ERR_UNSUPPORTED, "sparse_readout: problem too large for one launch");
     const hipError_t e = wf::launch_sparse_readout(dtype, vec, fast, p, stream);
     if (e != hipSuccess) return hip_fail("sparse_readout: kernel launch", e);
+    return WF_OK;
+}
+
+// ---- scratch of the entry point that allocates nothing (wf_fused_topk_sparse_fwd_noalloc)
+// The fused forward's only scratch is the retrieval's per-chunk key magnitude bounds:
+// B * ceil(T / 256) floats, every one written by the magnitude kernel before the retrieval
+// reads it, so nothing needs clearing. Each device holds its own copy of this array until
+// the process ends; calls that overlap on one device share it and race.
+constexpr size_t kScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+void* g_scratch_ptr[kMaxScratchDevices];
+hipError_t g_scratch_err[kMaxScratchDevices];
+std::once_flag g_scratch_once[kMaxScratchDevices];
+
+// Device address of `scratch` on the current device, looked up once per device with that
+// device current. The array's name is only a host-side handle; kernels get this address.
+int scratch_for_current_device(void** out)
+{
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail("fused_noalloc: hipGetDevice", e);
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(WF_ERR_UNSUPPORTED, "fused_noalloc: device %d beyond the %d supported", dev, kMaxScratchDevices);
+    std::call_once(g_scratch_once[dev], [dev] {
+        void* ptr = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+    });
+    if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
+        return hip_fail("fused_noalloc: hipGetSymbolAddress(scratch)", g_scratch_err[dev]);
+    *out = g_scratch_ptr[dev];
     return WF_OK;
 }
 
@@ -499,6 +533,26 @@ int wf_fused_topk_sparse_fwd(const wf_fused_args* a, void* stream)
 {
     const int rc = fused_run(a, a ? a->workspace : nullptr, a ? a->workspace_bytes : 0,
                              static_cast<hipStream_t>(stream));
+    return rc == WF_OK ? ok() : rc;
+}
+
+size_t wf_fused_noalloc_scratch_limit(void) { return kScratchBytes; }
+
+int wf_fused_topk_sparse_fwd_noalloc(const wf_fused_args* a, void* stream)
+{
+    if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "fused_noalloc: NULL argument struct");
+    const size_t need = wf_fused_workspace_bytes(a->B, a->T, a->R, a->top_k);
+    if (need > kScratchBytes)
+        return fail(WF_ERR_UNSUPPORTED, "fused_noalloc: this shape needs %zu bytes of scratch; the library's "
+                                        "scratch holds %zu (B * ceil(T / 256) <= %zu); use "
+                                        "wf_fused_topk_sparse_fwd with a workspace instead",
+                    need, kScratchBytes, kScratchBytes / sizeof(float));
+    void* ws = nullptr;
+    if (need > 0) {
+        const int rc = scratch_for_current_device(&ws);
+        if (rc != WF_OK) return rc;
+    }
+    const int rc = fused_run(a, ws, kScratchBytes, static_cast<hipStream_t>(stream));
     return rc == WF_OK ? ok() : rc;
 }
 

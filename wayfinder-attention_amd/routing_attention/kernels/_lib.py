@@ -78,6 +78,8 @@ SIGNATURES = {
                                               _i64p, _p]),
     "wf_fused_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "wf_fused_topk_sparse_fwd": (ctypes.c_int, [ctypes.POINTER(FusedArgs), _p]),
+    "wf_fused_noalloc_scratch_limit": (ctypes.c_size_t, []),
+    "wf_fused_topk_sparse_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(FusedArgs), _p]),
     "wf_probe_gather_sink_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "wf_probe_gather": (ctypes.c_int, [_p, _p, ctypes.c_int, _i64, _i64, _i64, _i64, _i64p, _i64p,
                                        _p, _i64p, _i64, _p, ctypes.c_size_t, _p]),
