@@ -321,6 +321,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
     ap.add_argument("--cpu-runs", type=int, default=3, help="timed runs of the CPU baseline")
+    ap.add_argument("--fused-pass", default="auto", choices=["auto", "split", "single"],
+                    help="fused forward as two kernels (split), one kernel (single) or the library's choice")
     ap.add_argument("--leg", default="all", choices=["all", "topk", "readout", "backward", "copy", "gather"],
                     help="profiling aid: run only one kernel (or a 256 MiB device copy used to "
                          "calibrate the FETCH_SIZE / WRITE_SIZE counters, or the readout against "
@@ -345,8 +347,13 @@ def main():
     s = torch.tensor([], dtype=dtype).element_size()
     path_bytes, readout_bytes = algorithmic_bytes(B, H, T, D, R, K, s)
 
+    from routing_attention.kernels import SparseMeatConfig
+
+    mcfg = SparseMeatConfig(fused_pass=args.fused_pass)
+
     def step():
-        return fused_sparse_attention(dev["qa"], dev["ka"], dev["q"], dev["k"], dev["v"], K, scale)
+        return fused_sparse_attention(dev["qa"], dev["ka"], dev["q"], dev["k"], dev["v"], K, scale,
+                                      meat_config=mcfg)
 
     if args.leg != "all":
         run_leg(args, dev, K, scale, readout_bytes)
@@ -410,7 +417,7 @@ def main():
         "data": f"synthetic ({dist} inputs from a fixed seed, resident in HBM)",
         "config": {"workload": f"fused causal top-K + sparse attention fwd, config {args.config[1:]}",
                    "B": B, "H": H, "T": T, "head_dim": D, "d_A": R, "top_k": K,
-                   "qkv_memory": "(B,T,H,D)", "parallelism": "single GPU"},
+                   "qkv_memory": "(B,T,H,D)", "fused_pass": args.fused_pass, "parallelism": "single GPU"},
         "latency_ms": lat,
         "pipelined_ms_per_call": round(ms, 4),
         "rows_per_s": round(B * T / (ms * 1e-3), 1),

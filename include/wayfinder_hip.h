@@ -52,6 +52,13 @@ typedef enum wf_dtype {
                                   by the retrieval) get zero weight. Off = reference
                                   behaviour: pads are attended (causal_topk.py:37-57). */
 
+/* Fused-forward pass selection (wf_fused_args.flags). Without either, the library picks. */
+#define WF_FLAG_SPLIT_PASS 0x2u  /* retrieval kernel, then readout kernel                      */
+#define WF_FLAG_SINGLE_PASS 0x4u /* one kernel: each workgroup retrieves 16 query rows and reads
+                                    them out for every head (WF_ERR_UNSUPPORTED unless bf16,
+                                    R = 32, 64 < k_eff <= 256, D in {64, 128}, H * D in
+                                    {512, 1024}, 16-byte aligned rows, contiguous head dim)     */
+
 /* Library ABI version (WF_ABI_VERSION of the build). No reference counterpart. */
 int wf_abi_version(void);
 

@@ -247,3 +247,24 @@ def test_probe_gather_contract_errors(lib):
     assert call(idx=FAKE + 4) == _lib.WF_ERR_UNSUPPORTED and "fast layout" in _lib.last_error()
     assert call(sink=16) == _lib.WF_ERR_WORKSPACE
     assert lib.wf_probe_gather_sink_bytes(1, 8, 64) == 8 * 4 * 256 * 4   # 8 pairs x 4 workgroups of 16 rows
+
+
+def test_fused_pass_flags_contract(lib):
+    """WF_FLAG_SINGLE_PASS on a shape the single-pass kernel does not take, and both pass
+    flags at once, are reported before any kernel launch."""
+    a = _lib.FusedArgs()
+    a.q_search = a.k_search = a.q = a.k = a.v = a.out = a.out_idx = FAKE
+    a.workspace, a.workspace_bytes = FAKE, 1 << 20
+    B, H, T, D, R = 1, 2, 64, 32, 32
+    a.qs_strides[:] = [T * R, R, 1]
+    a.ks_strides[:] = [T * R, R, 1]
+    for name in ("q_strides", "k_strides", "v_strides", "out_strides"):
+        getattr(a, name)[:] = [T * H * D, D, H * D, 1]
+    a.B, a.H, a.T, a.D, a.R, a.top_k = B, H, T, D, R, 16
+    a.search_dtype = a.dtype = 2
+    a.scale = 0.1
+    a.flags = _lib.WF_FLAG_SINGLE_PASS
+    assert lib.wf_fused_topk_sparse_fwd(ctypes.byref(a), None) == _lib.WF_ERR_UNSUPPORTED
+    assert "single-pass" in _lib.last_error()
+    a.flags = _lib.WF_FLAG_SINGLE_PASS | _lib.WF_FLAG_SPLIT_PASS
+    assert lib.wf_fused_topk_sparse_fwd(ctypes.byref(a), None) == _lib.WF_ERR_INVALID_ARGUMENT

@@ -278,6 +278,10 @@ int scratch_for_current_device(void** out)
     return WF_OK;
 }
 
+// Whether the fused forward takes the single-pass kernel where it applies and no flag forces
+// a mode (measured against the split path at configs 3, 4 and 5).
+constexpr bool kSinglePassDefault = false;
+
 // Validation and launches of the fused forward with the workspace `ws` (the caller's, or
 // the library's own scratch for the entry point that allocates nothing).
 int fused_run(const wf_fused_args* a, void* ws, size_t ws_bytes, hipStream_t s)
@@ -311,8 +315,34 @@ int fused_run(const wf_fused_args* a, void* ws, size_t ws_bytes, hipStream_t s)
                                   a->out_strides, nullptr, rp, &rvec, &rfast))
         return fail(WF_ERR_UNSUPPORTED, "fused: problem too large for one launch");
 
+    // single pass (one kernel: retrieval, then the block's rows read out for every head) or
+    // split (retrieval kernel, then readout kernel); WF_FLAG_SPLIT_PASS / WF_FLAG_SINGLE_PASS
+    // force one, otherwise kSinglePassDefault decides where both apply
+    wf::FusedReadoutParams fr{};
+    fr.q = a->q; fr.k = a->k; fr.v = a->v; fr.out = a->out;
+    for (int i = 0; i < 4; ++i) {
+        fr.qs[i] = a->q_strides[i]; fr.ks[i] = a->k_strides[i];
+        fr.vs[i] = a->v_strides[i]; fr.os[i] = a->out_strides[i];
+    }
+    fr.H = H; fr.D = a->D; fr.scale = a->scale; fr.flags = a->flags & WF_FLAG_MASK_PADS;
+    const bool single_ok = H > 0 && a->dtype == a->search_dtype && rvec &&
+                           wf::fused_single_pass_supported(a->dtype, tvec, tp, fr);
+    const unsigned mode = a->flags & (WF_FLAG_SPLIT_PASS | WF_FLAG_SINGLE_PASS);
+    if (mode == (WF_FLAG_SPLIT_PASS | WF_FLAG_SINGLE_PASS))
+        return fail(WF_ERR_INVALID_ARGUMENT, "fused: WF_FLAG_SPLIT_PASS and WF_FLAG_SINGLE_PASS are exclusive");
+    if (mode == WF_FLAG_SINGLE_PASS && !single_ok)
+        return fail(WF_ERR_UNSUPPORTED, "fused: the single-pass kernel needs bf16 addresses and q/k/v, R = 32, "
+                                        "64 < k_eff <= 256, D in {64, 128}, H * D in {512, 1024} and 16-byte "
+                                        "aligned rows with a contiguous head dim");
+    const bool single = mode == WF_FLAG_SINGLE_PASS || (mode == 0 && single_ok && kSinglePassDefault);
+
     hipError_t e = wf::launch_key_absmax(a->search_dtype, tvec, tp, s);
     if (e != hipSuccess) return hip_fail("fused: key magnitude kernel launch", e);
+    if (single) {
+        e = wf::launch_fused_single_pass(a->dtype, tp, fr, s);
+        if (e != hipSuccess) return hip_fail("fused: single-pass kernel launch", e);
+        return WF_OK;
+    }
     e = wf::launch_causal_topk(a->search_dtype, tvec, tp, s);
     if (e != hipSuccess) return hip_fail("fused: retrieval kernel launch", e);
     if (H == 0) return WF_OK;   // no heads: the indices are still the result's second half

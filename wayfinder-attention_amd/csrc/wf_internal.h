@@ -134,6 +134,19 @@ struct ReadoutParams {
                             // set by the launcher from the kernel's occupancy
 };
 
+// Readout stage of the single-pass fused kernel (wf_fused.hip): the block's rows for all
+// heads, right after their retrieval.
+struct FusedReadoutParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    int64_t qs[4], ks[4], vs[4], os[4];   // element strides (B, H, T, D); stride of D is 1
+    int64_t H, D;
+    float scale;
+    unsigned flags;                        // bit 0: mask the pad slots
+};
+
 // Backward of the readout (fixed indices). Both passes pair blockIdx % 8 with a fixed set of
 // (b, h) pairs at every grid size (the row pass over query rows t, the key pass over key rows
 // j): chunk-major order starts the key pass's long early-key lists of every pair first, which
@@ -202,6 +215,11 @@ hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutPa
 size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K);
 hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_address_project(int dtype, const AddressParams& p, hipStream_t s);
+// single-pass fused forward (wf_fused.hip): retrieval and all-heads readout in one kernel.
+// True if the shape and layout qualify (16-bit types, R = 32 on the aligned path,
+// 64 < k_eff <= 256, D / 8 lanes per head with H * D / 8 in {64, 128}).
+bool fused_single_pass_supported(int dtype, bool topk_vec, const TopkParams& tp, const FusedReadoutParams& fr);
+hipError_t launch_fused_single_pass(int dtype, const TopkParams& tp, const FusedReadoutParams& fr, hipStream_t s);
 // measurement aid (wf_probe.hip): the readout's gathers without its arithmetic, 16-bit types
 hipError_t launch_gather_probe(int dtype, const ReadoutParams& p, uint32_t* sink, hipStream_t s);
 

@@ -25,6 +25,8 @@ WF_ERR_HIP = 4
 
 WF_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 WF_FLAG_MASK_PADS = 0x1
+WF_FLAG_SPLIT_PASS = 0x2
+WF_FLAG_SINGLE_PASS = 0x4
 
 # Exported symbols and their C signatures (kept in step with include/wayfinder_hip.h).
 _i64 = ctypes.c_int64

@@ -26,9 +26,11 @@ class SparseMeatConfig:
     """Launch options for the readout (reference fused_sparse.py:30-38).
 
     method / block_d / k_pad / num_warps / compute_dtype are accepted for compatibility;
-    the HIP kernel picks its own tiling. ``mask_pads`` is this build's addition: give zero
+    the HIP kernel picks its own tiling. This build's additions: ``mask_pads`` gives zero
     weight to the pad slots (s > t) of rows t < K-1 instead of attending them as the
-    reference does.
+    reference does; ``fused_pass`` selects how fused_sparse_attention runs -- "split"
+    (retrieval kernel, then readout kernel), "single" (one kernel that retrieves each block
+    of 16 query rows and reads them out for every head) or "auto" (the library's choice).
     """
 
     method: str = "auto"
@@ -37,6 +39,7 @@ class SparseMeatConfig:
     num_warps: int = 4
     compute_dtype: str | None = None
     mask_pads: bool = False
+    fused_pass: str = "auto"
 
 
 def _resolve_sparse_meat_config(T: int, H: int, D: int, k_eff: int,
@@ -50,6 +53,7 @@ def _resolve_sparse_meat_config(T: int, H: int, D: int, k_eff: int,
         num_warps=cfg.num_warps,
         compute_dtype=cfg.compute_dtype,
         mask_pads=cfg.mask_pads,
+        fused_pass=cfg.fused_pass,
     )
 
 
@@ -67,8 +71,15 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise ValueError(f"q/k/v dtype mismatch: {q.dtype} {k.dtype} {v.dtype}")
 
 
+_PASS_FLAGS = {"auto": 0, "split": _lib.WF_FLAG_SPLIT_PASS, "single": _lib.WF_FLAG_SINGLE_PASS}
+
+
 def _flags(cfg: SparseMeatConfig | None) -> int:
-    return _lib.WF_FLAG_MASK_PADS if (cfg is not None and cfg.mask_pads) else 0
+    if cfg is None:
+        return 0
+    if cfg.fused_pass not in _PASS_FLAGS:
+        raise ValueError(f"fused_pass must be one of {sorted(_PASS_FLAGS)}, got {cfg.fused_pass!r}")
+    return (_lib.WF_FLAG_MASK_PADS if cfg.mask_pads else 0) | _PASS_FLAGS[cfg.fused_pass]
 
 
 @torch.no_grad()
