@@ -323,7 +323,7 @@ def main():
     ap.add_argument("--cpu-runs", type=int, default=3, help="timed runs of the CPU baseline")
     ap.add_argument("--fused-pass", default="auto", choices=["auto", "split", "single"],
                     help="fused forward as two kernels (split), one kernel (single) or the library's choice")
-    ap.add_argument("--leg", default="all", choices=["all", "topk", "readout", "backward", "copy", "gather"],
+    ap.add_argument("--leg", default="all", choices=["all", "fused", "topk", "readout", "backward", "copy", "gather"],
                     help="profiling aid: run only one kernel (or a 256 MiB device copy used to "
                          "calibrate the FETCH_SIZE / WRITE_SIZE counters, or the readout against "
                          "its gather-path probe) and print its timing")
@@ -355,6 +355,10 @@ def main():
         return fused_sparse_attention(dev["qa"], dev["ka"], dev["q"], dev["k"], dev["v"], K, scale,
                                       meat_config=mcfg)
 
+    if args.leg == "fused":
+        ms = time_loop(step, args.steps, args.warmup)
+        print(json.dumps({"leg": "fused", "fused_pass": args.fused_pass, "ms": round(ms, 4)}), flush=True)
+        return
     if args.leg != "all":
         run_leg(args, dev, K, scale, readout_bytes)
         return
