@@ -83,7 +83,7 @@ size_t wf_causal_topk_workspace_bytes(int64_t B, int64_t T, int64_t R, int64_t t
  * out_scores : optional (B, T, k_eff) float32 (NULL to skip): the fp32 score of every
  *              slot, -inf in pad slots.
  * workspace  : device buffer of at least wf_causal_topk_workspace_bytes(...) bytes.
- * Limits: 1 <= R <= 128, 1 <= top_k (k_eff <= 256), T < 2^31.
+ * Limits: 1 <= R <= 256, 1 <= top_k (k_eff <= 512), T < 2^31.
  */
 int wf_causal_topk_fwd(const void* query, const void* key, int dtype,
                        int64_t B, int64_t T, int64_t R,
@@ -103,7 +103,7 @@ int wf_causal_topk_fwd(const void* query, const void* key, int dtype,
  *            out[b,h,t] = sum_s softmax_s(scale * q[b,h,t].k[b,h,idx[b,t,s]]) v[b,h,idx[b,t,s]]
  *            computed in fp32, rounded once to `dtype`.
  * flags    : WF_FLAG_MASK_PADS or 0.
- * Limits: D in {32, 64, 128}, 1 <= K <= 1024.
+ * Limits: 1 <= D <= 256, 1 <= K <= 1024.
  */
 int wf_sparse_readout_fwd(const void* q, const void* k, const void* v, int dtype,
                           int64_t B, int64_t H, int64_t T, int64_t D,
@@ -171,7 +171,7 @@ size_t wf_sparse_readout_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, in
  * fp32 accumulation, deterministic (no floating-point atomics), one rounding per element.
  * Layout: every (B, H, T, D) tensor with contiguous head dim, 16-byte aligned rows and a
  * per-(b, h) span below 4 GiB (the (B, T, H, D) memory of the module qualifies);
- * otherwise WF_ERR_UNSUPPORTED. Limits: D in {32, 64, 128}, 1 <= K <= 1024,
+ * otherwise WF_ERR_UNSUPPORTED. Limits: D a multiple of 8 up to 256, 1 <= K <= 1024,
  * B*T*K < 2^32.
  */
 int wf_sparse_readout_bwd(const wf_readout_bwd_args* args, void* stream);

@@ -61,8 +61,8 @@ def _topk(lib, **kw):
     (dict(R=0), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
     (dict(T=-1), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
     (dict(top_k=-3), _lib.WF_ERR_INVALID_ARGUMENT, "top_k"),
-    (dict(R=129), _lib.WF_ERR_UNSUPPORTED, "R=129"),
-    (dict(top_k=300, T=1000), _lib.WF_ERR_UNSUPPORTED, "k_eff"),
+    (dict(R=257), _lib.WF_ERR_UNSUPPORTED, "R=257"),
+    (dict(top_k=600, T=1000), _lib.WF_ERR_UNSUPPORTED, "k_eff"),
     (dict(query=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
     (dict(out=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
     (dict(qs=None), _lib.WF_ERR_INVALID_ARGUMENT, "stride"),
@@ -109,7 +109,7 @@ def _readout(lib, **kw):
 
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(dtype=-1), _lib.WF_ERR_UNSUPPORTED, "dtype"),
-    (dict(D=48), _lib.WF_ERR_UNSUPPORTED, "head_dim"),
+    (dict(D=300), _lib.WF_ERR_UNSUPPORTED, "head_dim"),
     (dict(K=0), _lib.WF_ERR_INVALID_ARGUMENT, "K must"),
     (dict(K=5000), _lib.WF_ERR_UNSUPPORTED, "K=5000"),
     (dict(H=-2), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
@@ -137,7 +137,7 @@ def test_fused_contract_errors(lib):
         getattr(a, f)[:] = [8 * 64 * 64, 64 * 64, 64, 1]
     a.B, a.H, a.T, a.D, a.R, a.top_k = 1, 8, 64, 64, 32, 8
     a.search_dtype, a.dtype, a.scale = 2, 2, 0.125
-    a.D = 40
+    a.D = 300
     assert lib.wf_fused_topk_sparse_fwd(ctypes.byref(a), None) == _lib.WF_ERR_UNSUPPORTED
     a.D, a.top_k = 64, 0
     assert lib.wf_fused_topk_sparse_fwd(ctypes.byref(a), None) == _lib.WF_ERR_INVALID_ARGUMENT
@@ -177,7 +177,7 @@ def _bwd(lib, **kw):
 
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(dtype=7), _lib.WF_ERR_UNSUPPORTED, "dtype"),
-    (dict(D=48), _lib.WF_ERR_UNSUPPORTED, "head_dim"),
+    (dict(D=300), _lib.WF_ERR_UNSUPPORTED, "head_dim"),
     (dict(K=0), _lib.WF_ERR_INVALID_ARGUMENT, "K must be"),
     (dict(K=2000), _lib.WF_ERR_UNSUPPORTED, "K=2000"),
     (dict(dout=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),

@@ -95,8 +95,9 @@ int64_t gcd64(int64_t a, int64_t b)
     return a;
 }
 
-constexpr int64_t kMaxTopK = 256;
-constexpr int64_t kMaxR = 128;
+constexpr int64_t kMaxTopK = 512;
+constexpr int64_t kMaxR = 256;
+constexpr int64_t kMaxD = 256;
 constexpr int64_t kMaxReadoutK = 1024;
 
 int check_topk(const void* query, const void* key, int dtype, int64_t B, int64_t T, int64_t R,
@@ -122,7 +123,7 @@ int check_readout(const void* q, const void* k, const void* v, int dtype, int64_
 {
     if (!valid_dtype(dtype)) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: unsupported dtype code %d", dtype);
     if (B < 0 || H < 0 || T < 0 || D < 1) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout: bad shape (B=%lld, H=%lld, T=%lld, D=%lld)", (long long)B, (long long)H, (long long)T, (long long)D);
-    if (D != 32 && D != 64 && D != 128) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: head_dim %lld not in {32, 64, 128}", (long long)D);
+    if (D > kMaxD) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: head_dim %lld > %lld", (long long)D, (long long)kMaxD);
     if (K < 1) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout: K must be >= 1, got %lld", (long long)K);
     if (K > kMaxReadoutK) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: K=%lld > %lld", (long long)K, (long long)kMaxReadoutK);
     if (T >= (int64_t(1) << 31) - 1) return fail(WF_ERR_UNSUPPORTED, "sparse_readout: T=%lld does not fit int32 indices", (long long)T);
@@ -154,8 +155,8 @@ bool topk_prepare(const void* query, const void* key, int dtype, int64_t B, int6
     p.rb_end = p.n_row_blocks;
     p.n_cus = wf::device_cu_count();
     // vector loads; key rows are addressed with 32-bit byte offsets from the batch base and
-    // every 32-dim chunk the kernel reads lies inside the row (R = 32, 64 or 128)
-    return (R == 32 || R == 64 || R == 128) &&
+    // every 32-dim chunk the kernel reads lies inside the row (R = 32, 64, 128 or 256)
+    return (R == 32 || R == 64 || R == 128 || R == 256) &&
            vec_ok(query, dtype, qs, 3, R) && vec_ok(key, dtype, ks, 3, R) &&
            ks[1] >= 0 && (T - 1) * ks[1] * int64_t(elem_size(dtype)) + R * int64_t(elem_size(dtype)) < (int64_t(1) << 32);
 }

@@ -209,6 +209,9 @@ int64_t resident_workgroups(const void* kernel, int block);
 // launchers (return hipError_t of the launch)
 hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s);
+hipError_t launch_causal_topk_bf16(bool vec, const TopkParams& p, hipStream_t s);
+hipError_t launch_causal_topk_f16(bool vec, const TopkParams& p, hipStream_t s);
+hipError_t launch_causal_topk_f32(bool vec, const TopkParams& p, hipStream_t s);
 hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutParams& p, hipStream_t s);
 // device workspace of the backward for this shape (index transpose arrays, radix histograms,
 // per-row statistics); a function of the shape only

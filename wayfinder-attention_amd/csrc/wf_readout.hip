@@ -50,7 +50,9 @@ struct Stage {
     uint4 qlo, qhi;
 };
 
-// D: head dim (32, 64, 128); NB: wave steps per task.
+// D: the lane layout's head dim (32, 64, 128, 256); the problem's p.D is any value up to D
+// (lanes holding dims past p.D read zeros and store nothing; a slice the head dim ends in is
+// read and written element by element). NB: wave steps per task.
 template <typename DT, bool VEC, int D, int NB>
 __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutParams p)
 {
@@ -82,10 +84,24 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
     const bool mask_flag = (p.flags & 1u) != 0;
     const float sl2 = p.scale * kLog2e;   // scale multiplies the finished dot, as in the reference
 
-    const DT* qbase = static_cast<const DT*>(p.q) + b * p.qs[0] + h * p.qs[1] + int64_t(sub) * 8 * p.qs[3];
-    const DT* kbase = static_cast<const DT*>(p.k) + b * p.ks[0] + h * p.ks[1] + int64_t(sub) * 8 * p.ks[3];
-    const DT* vbase = static_cast<const DT*>(p.v) + b * p.vs[0] + h * p.vs[1] + int64_t(sub) * 8 * p.vs[3];
+    const int nd = min(8, int(p.D) - sub * 8);   // dims of this lane's slice (<= 0: none)
+    const int sl = nd > 0 ? sub : 0;             // slice addressed (in bounds for idle lanes)
+    const DT* qbase = static_cast<const DT*>(p.q) + b * p.qs[0] + h * p.qs[1] + int64_t(sl) * 8 * p.qs[3];
+    const DT* kbase = static_cast<const DT*>(p.k) + b * p.ks[0] + h * p.ks[1] + int64_t(sl) * 8 * p.ks[3];
+    const DT* vbase = static_cast<const DT*>(p.v) + b * p.vs[0] + h * p.vs[1] + int64_t(sl) * 8 * p.vs[3];
     const int32_t* ibase = p.idx + b * p.is[0];
+    // one slice: a 16-byte vector when the layout allows and the slice is whole, else the
+    // slice's first nd elements one by one; zeros for lanes past the head dim
+    auto load_slice = [&](const DT* ptr, int64_t sd, uint4& lo, uint4& hi) {
+        if (nd >= 8) {
+            load_row8<DT, VEC>(ptr, sd, lo, hi);
+        } else if (nd > 0) {
+            load_row8_part<DT>(ptr, sd, nd, lo, hi);
+        } else {
+            lo = make_uint4(0, 0, 0, 0);
+            hi = lo;
+        }
+    };
 
     auto fetch_idx = [&](int tau, Stage<NB>& st) {
         const int64_t t = tw + tau / nb;
@@ -101,14 +117,14 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
             if (j < 0) j += T;
             st.j[u] = int(j < 0 ? 0 : (j > T - 1 ? T - 1 : j));
         }
-        if (bat == 0) load_row8<DT, VEC>(qbase + t * p.qs[2], p.qs[3], st.qlo, st.qhi);
+        if (bat == 0) load_slice(qbase + t * p.qs[2], p.qs[3], st.qlo, st.qhi);
     };
     auto fetch_kv = [&](const Stage<NB>& st, uint4 (&klo)[NB], uint4 (&khi)[NB], uint4 (&vlo)[NB],
                         uint4 (&vhi)[NB]) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            load_row8<DT, VEC>(kbase + int64_t(st.j[u]) * p.ks[2], p.ks[3], klo[u], khi[u]);
-            load_row8<DT, VEC>(vbase + int64_t(st.j[u]) * p.vs[2], p.vs[3], vlo[u], vhi[u]);
+            load_slice(kbase + int64_t(st.j[u]) * p.ks[2], p.ks[3], klo[u], khi[u]);
+            load_slice(vbase + int64_t(st.j[u]) * p.vs[2], p.vs[3], vlo[u], vhi[u]);
         }
     };
 
@@ -162,8 +178,9 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o8[e] *= inv;
                 const int64_t t = tw + tau / nb;
-                DT* op = static_cast<DT*>(p.out) + b * p.os[0] + h * p.os[1] + t * p.os[2] + int64_t(sub) * 8 * p.os[3];
-                store_row8<DT, VEC>(op, p.os[3], o8);
+                DT* op = static_cast<DT*>(p.out) + b * p.os[0] + h * p.os[1] + t * p.os[2] + int64_t(sl) * 8 * p.os[3];
+                if (nd >= 8) store_row8<DT, VEC>(op, p.os[3], o8);
+                else if (nd > 0) store_row8_part<DT>(op, p.os[3], nd, o8);
                 if (p.lse2 && sub == 0) p.lse2[(b * p.H + h) * T + t] = m + log2f(lt);
             }
         }
@@ -209,6 +226,10 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 // indices arrive in one 16-byte load per task instead of one 4-byte load per step (a quarter
 // of the vector-memory instructions); needs
 // K % 4 == 0, 16-byte aligned index rows and K >= NB (checked by the launcher).
+// D: the lane layout's head dim (32, 64, 128, 256); the problem's head dim p.D may be any
+// multiple of 8 up to D. Lanes past p.D / 8 load the row's last slice (so no load is
+// conditional), zero their query slice (so they add nothing to any dot product) and store
+// nothing.
 template <typename DT, int D, int NB, bool LSE, bool TRUST, bool VI>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(sizeof(DT) == 2 && !LSE ? 4 : 1)))
 void sparse_readout_fast(ReadoutParams p)
@@ -248,7 +269,9 @@ void sparse_readout_fast(ReadoutParams p)
     char* ob = reinterpret_cast<char*>(static_cast<DT*>(p.out) + b * p.os[0] + h * p.os[1] + tw * p.os[2]);
     const uint32_t krow = uint32_t(p.ks[2]) * ES, vrow = uint32_t(p.vs[2]) * ES;
     const uint32_t qrow = uint32_t(p.qs[2]) * ES, orow = uint32_t(p.os[2]) * ES;
-    const uint32_t loff = uint32_t(sub) * 8u * ES;
+    const int dv = int(p.D) / 8;                     // active lanes per neighbour
+    const bool lane_on = sub < dv;
+    const uint32_t loff = uint32_t(min(sub, dv - 1)) * 8u * ES;
     const int32_t* ib = p.idx + b * p.is[0] + tw * p.is[1];
     float* lrow = LSE ? p.lse2 + (b * p.H + h) * p.T + tw : nullptr;   // wave-uniform
     const int64_t irow = p.is[1];
@@ -289,6 +312,7 @@ void sparse_readout_fast(ReadoutParams p)
     for (int r = 0; r < kRowsPerWave; ++r) {
         uint4 lo, hi;
         ld16<DT>(qb, uint32_t(min(r, nrows - 1)) * qrow + loff, lo, hi);
+        if (!lane_on) { lo = make_uint4(0, 0, 0, 0); hi = lo; }   // past the head dim
         sq[wave][r][0][lane] = lo;
         if constexpr (QW == 2) sq[wave][r][QW - 1][lane] = hi;
     }
@@ -351,7 +375,7 @@ void sparse_readout_fast(ReadoutParams p)
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o8[e] *= inv;
-                store_row8<DT, true>(reinterpret_cast<DT*>(ob + uint32_t(rc) * orow + loff), 1, o8);
+                if (lane_on) store_row8<DT, true>(reinterpret_cast<DT*>(ob + uint32_t(rc) * orow + loff), 1, o8);
                 if (LSE && sub == 0) lrow[rc] = mm + log2f(lt);
             }
         }
@@ -447,12 +471,14 @@ hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
     return launch_readout<sparse_readout_fast<DT, D, NB, false, false, false>>(p, s);
 }
 
+// Lane layout for head dim D: D / 8 lanes per neighbour, padded to a power of two >= 4.
 template <typename DT>
 hipError_t launch_fast_t(const ReadoutParams& p, hipStream_t s)
 {
-    if (p.D == 32) return launch_fast_d<DT, 32>(p, s);
-    if (p.D == 64) return launch_fast_d<DT, 64>(p, s);
-    return launch_fast_d<DT, 128>(p, s);
+    if (p.D <= 32) return launch_fast_d<DT, 32>(p, s);
+    if (p.D <= 64) return launch_fast_d<DT, 64>(p, s);
+    if (p.D <= 128) return launch_fast_d<DT, 128>(p, s);
+    return launch_fast_d<DT, 256>(p, s);
 }
 
 template <typename DT, bool VEC, int D>
@@ -468,9 +494,10 @@ hipError_t launch_d(const ReadoutParams& p, hipStream_t s)
 template <typename DT, bool VEC>
 hipError_t launch_v(const ReadoutParams& p, hipStream_t s)
 {
-    if (p.D == 32) return launch_d<DT, VEC, 32>(p, s);
-    if (p.D == 64) return launch_d<DT, VEC, 64>(p, s);
-    return launch_d<DT, VEC, 128>(p, s);
+    if (p.D <= 32) return launch_d<DT, VEC, 32>(p, s);
+    if (p.D <= 64) return launch_d<DT, VEC, 64>(p, s);
+    if (p.D <= 128) return launch_d<DT, VEC, 128>(p, s);
+    return launch_d<DT, VEC, 256>(p, s);
 }
 
 template <typename DT>

@@ -296,7 +296,11 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
     const uint32_t krow = uint32_t(p.ks[2]) * ES, vrow = uint32_t(p.vs[2]) * ES;
     const uint32_t qrow = uint32_t(p.qs[2]) * ES, grow = uint32_t(p.gs[2]) * ES;
     const uint32_t drow = uint32_t(p.dqs[2]) * ES;
-    const uint32_t loff = uint32_t(sub) * 8u * ES;
+    // lanes past the head dim (p.D < D) read the last slice, zero their q / dout slices (no
+    // contribution to any dot product) and store nothing
+    const int dv = int(p.D) / 8;
+    const bool lane_on = sub < dv;
+    const uint32_t loff = uint32_t(min(sub, dv - 1)) * 8u * ES;
     const int32_t* ib = p.idx + b * p.is[0] + tw * p.is[1];
     const int64_t rbase = (b * p.H + h) * p.T + tw;
 
@@ -305,6 +309,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
         uint4 qlo, qhi, glo, ghi;
         ld16<DT>(qb, uint32_t(r) * qrow + loff, qlo, qhi);
         ld16<DT>(gb, uint32_t(r) * grow + loff, glo, ghi);
+        if (!lane_on) { qlo = make_uint4(0, 0, 0, 0); qhi = qlo; glo = qlo; ghi = qlo; }
         const float lt2 = p.lse2[rbase + r];
         const int lim = (mask_flag && t < K - 1) ? t + 1 : K;   // slots >= lim carry no weight
         const int32_t* ip = ib + r * p.is[1];
@@ -343,7 +348,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
             o8[e] = p.scale * (a - delta * bk);
         }
         if (grp == 0) {
-            store_row8<DT, true>(reinterpret_cast<DT*>(db + uint32_t(r) * drow + loff), 1, o8);
+            if (lane_on) store_row8<DT, true>(reinterpret_cast<DT*>(db + uint32_t(r) * drow + loff), 1, o8);
             if (sub == 0) p.row_stats[rbase + r] = make_float2(lt2, delta);
         }
     }
@@ -374,7 +379,9 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams
     const uint32_t qrow = uint32_t(p.qs[2]) * ES, grow = uint32_t(p.gs[2]) * ES;
     const uint32_t krow = uint32_t(p.ks[2]) * ES, vrow = uint32_t(p.vs[2]) * ES;
     const uint32_t dkrow = uint32_t(p.dks[2]) * ES, dvrow = uint32_t(p.dvs[2]) * ES;
-    const uint32_t loff = uint32_t(sub) * 8u * ES;
+    const int dv = int(p.D) / 8;   // lanes past the head dim: zero k / v slices, no stores
+    const bool lane_on = sub < dv;
+    const uint32_t loff = uint32_t(min(sub, dv - 1)) * 8u * ES;
     const float2* rs = p.row_stats + (b * p.H + h) * p.T;
     const uint32_t* off = p.off + b * p.T + jw;
 
@@ -382,6 +389,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams
         uint4 klo, khi, vlo, vhi;
         ld16<DT>(kb, uint32_t(r) * krow + loff, klo, khi);
         ld16<DT>(vb, uint32_t(r) * vrow + loff, vlo, vhi);
+        if (!lane_on) { klo = make_uint4(0, 0, 0, 0); khi = klo; vlo = klo; vhi = klo; }
         const uint32_t e0 = off[r], e1 = off[r + 1];
         float ak[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         float av[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -414,7 +422,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams
             ok8[c] = p.scale * group_allreduce<LPN, false>(ak[c]);
             ov8[c] = group_allreduce<LPN, false>(av[c]);
         }
-        if (grp == 0) {
+        if (grp == 0 && lane_on) {
             store_row8<DT, true>(reinterpret_cast<DT*>(dkb + uint32_t(r) * dkrow + loff), 1, ok8);
             store_row8<DT, true>(reinterpret_cast<DT*>(dvb + uint32_t(r) * dvrow + loff), 1, ov8);
         }
@@ -460,15 +468,19 @@ hipError_t launch_passes(const ReadoutBwdParams& p, hipStream_t s)
 {
     const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
     const dim3 g(static_cast<unsigned>(grid)), blk(64 * kWaves);
-    if (p.D == 32) {
+    // lane layout: the head dim padded to 32, 64, 128 or 256 (D / 8 lanes per neighbour)
+    if (p.D <= 32) {
         readout_bwd_rows<DT, 32><<<g, blk, 0, s>>>(p);
         readout_bwd_keys<DT, 32><<<g, blk, 0, s>>>(p);
-    } else if (p.D == 64) {
+    } else if (p.D <= 64) {
         readout_bwd_rows<DT, 64><<<g, blk, 0, s>>>(p);
         readout_bwd_keys<DT, 64><<<g, blk, 0, s>>>(p);
-    } else {
+    } else if (p.D <= 128) {
         readout_bwd_rows<DT, 128><<<g, blk, 0, s>>>(p);
         readout_bwd_keys<DT, 128><<<g, blk, 0, s>>>(p);
+    } else {
+        readout_bwd_rows<DT, 256><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 256><<<g, blk, 0, s>>>(p);
     }
     return hipGetLastError();
 }

@@ -38,6 +38,39 @@ __device__ __forceinline__ void load_row8(const DT* p, int64_t sd, uint4& lo, ui
     }
 }
 
+// Elements [0, n) of an 8-element slice at element stride sd (n < 8: the head dim ends
+// inside the slice); the rest read as zero. For layouts without 16-byte vector access.
+template <typename DT>
+__device__ __forceinline__ void load_row8_part(const DT* p, int64_t sd, int n, uint4& lo, uint4& hi)
+{
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (sizeof(DT) == 2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (e < n) w[e >> 1] |= uint32_t(*reinterpret_cast<const uint16_t*>(p + e * sd)) << (16 * (e & 1));
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (e < n) w[e] = __float_as_uint(*reinterpret_cast<const float*>(p + e * sd));
+    }
+    lo = make_uint4(w[0], w[1], w[2], w[3]);
+    hi = sizeof(DT) == 4 ? make_uint4(w[4], w[5], w[6], w[7]) : make_uint4(0, 0, 0, 0);
+}
+
+// Elements [0, n) of an 8-element slice written from f at element stride sd.
+template <typename DT>
+__device__ __forceinline__ void store_row8_part(DT* p, int64_t sd, int n, const float* f)
+{
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        if (e < n) {
+            DT v;
+            from_f32(f[e], v);
+            p[e * sd] = v;
+        }
+    }
+}
+
 template <typename DT>
 __device__ __forceinline__ void cvt8(const uint4& lo, const uint4& hi, float* f)
 {
@@ -71,11 +104,12 @@ __device__ __forceinline__ void store_row8(DT* p, int64_t sd, const float* f)
 }
 
 // ---------------------------------------------------------------- reductions
-// Sum over the LPN lanes that share one neighbour (LPN in {4, 8, 16}), with DPP: quad_perm
+// Sum over the LPN lanes that share one neighbour (LPN in {4, 8, 16, 32}), with DPP: quad_perm
 // xor 1 and xor 2 sum each quad; row_half_mirror then adds the other quad of the 8-lane
-// group and row_mirror the other half of the 16-lane row. Every pattern reads a valid lane,
-// so bound_ctrl changes nothing; written as update_dpp(0, x, ...) the compiler folds each
-// move into the add (one v_add_f32_dpp per level).
+// group and row_mirror the other half of the 16-lane row; for 32 lanes one shuffle adds the
+// other row. Every DPP pattern reads a valid lane, so bound_ctrl changes nothing; written as
+// update_dpp(0, x, ...) the compiler folds each move into the add (one v_add_f32_dpp per
+// level).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x)
 {
@@ -89,6 +123,7 @@ __device__ __forceinline__ float group_sum(float x)
     x += dpp<0x4E>(x);
     if constexpr (LPN >= 8) x += dpp<0x141>(x);
     if constexpr (LPN >= 16) x += dpp<0x140>(x);
+    if constexpr (LPN >= 32) x += __shfl_xor(x, 16, 64);
     return x;
 }
 
@@ -143,16 +178,16 @@ __device__ __forceinline__ float dpp_ror(float x)
 }
 
 // op over the lane groups of the wave (groups = lanes with equal bits below LPN): DPP
-// row_ror inside each 16-lane row, then xor-16 / xor-32 shuffles across rows. (The
-// gfx950 v_permlane{16,32}_swap builtins would avoid the shuffles, but this toolchain
-// folds their two results into one when both feed the same expression.)
+// row_ror inside each 16-lane row, then xor-16 / xor-32 shuffles across rows (xor-32 only
+// for 32-lane groups). (The gfx950 v_permlane{16,32}_swap builtins would avoid the shuffles,
+// but this toolchain folds their two results into one when both feed the same expression.)
 template <int LPN, bool MAX>
 __device__ __forceinline__ float group_allreduce(float x)
 {
     if constexpr (LPN <= 4) { const float y = dpp_ror<4>(x); x = MAX ? fmaxf(x, y) : x + y; }
     if constexpr (LPN <= 8) { const float y = dpp_ror<8>(x); x = MAX ? fmaxf(x, y) : x + y; }
 #pragma unroll
-    for (int o = 16; o < 64; o <<= 1) {
+    for (int o = LPN > 16 ? LPN : 16; o < 64; o <<= 1) {
         const float y = __shfl_xor(x, o, 64);
         x = MAX ? fmaxf(x, y) : x + y;
     }

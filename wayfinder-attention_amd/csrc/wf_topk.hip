@@ -1,5 +1,6 @@
-// wf_topk.hip -- causal top-K address retrieval for gfx950 (MI355X): kernels and
-// launchers. The algorithm and its device code are in wf_topk_dev.h.
+// wf_topk.hip -- causal top-K address retrieval for gfx950 (MI355X): the key-magnitude
+// kernel and the launchers. The algorithm and its device code are in wf_topk_dev.h, the
+// retrieval kernels' instantiations in wf_topk_inst.h (one translation unit per type).
 //
 // Replaces routing_attention/kernels/causal_topk.py:132-171 (_causal_topk_row_blocked) and
 // :37-57 (_finalize_causal_topk).
@@ -39,52 +40,6 @@ __global__ __launch_bounds__(kAbsmaxChunk) void key_absmax_kernel(TopkParams p)
     }
 }
 
-// Two workgroups per CU: LDS (<= 80 KiB each) and registers (<= 256 per lane) both allow 2
-// waves per SIMD for address dims up to 64; the attribute keeps the register allocation
-// inside that bound. Wider addresses (RC = 4) keep their registers at 1 wave per SIMD.
-template <typename DT, bool VEC, int RC, int KP2>
-__global__ __launch_bounds__(64 * kTopkWaves) __attribute__((amdgpu_waves_per_eu(2)))
-void causal_topk_kernel(TopkParams p)
-{
-    causal_topk_body<DT, VEC, RC, KP2>(p);
-}
-template <typename DT, bool VEC, int RC, int KP2>
-__global__ __launch_bounds__(64 * kTopkWaves) void causal_topk_wide_kernel(TopkParams p)
-{
-    causal_topk_body<DT, VEC, RC, KP2>(p);
-}
-
-template <typename DT, bool VEC, int RC, int KP2>
-void launch_topk_kp(const TopkParams& p, hipStream_t s)
-{
-    const dim3 grid(unsigned(p.B * (p.rb_end - p.rb_begin))), block(64 * kTopkWaves);
-    if constexpr (RC <= 2) causal_topk_kernel<DT, VEC, RC, KP2><<<grid, block, 0, s>>>(p);
-    else causal_topk_wide_kernel<DT, VEC, RC, KP2><<<grid, block, 0, s>>>(p);
-}
-
-template <typename DT, bool VEC, int RC>
-hipError_t launch_topk_k(const TopkParams& p, hipStream_t s)
-{
-    if (p.k_eff <= 64) launch_topk_kp<DT, VEC, RC, 64>(p, s);
-    else if (p.k_eff <= 128) launch_topk_kp<DT, VEC, RC, 128>(p, s);
-    else launch_topk_kp<DT, VEC, RC, 256>(p, s);
-    return hipGetLastError();
-}
-
-template <typename DT, bool VEC>
-hipError_t launch_topk_r(const TopkParams& p, hipStream_t s)
-{
-    if (p.R <= 32) return launch_topk_k<DT, VEC, 1>(p, s);
-    if (p.R <= 64) return launch_topk_k<DT, VEC, 2>(p, s);
-    return launch_topk_k<DT, VEC, 4>(p, s);
-}
-
-template <typename DT>
-hipError_t launch_topk_t(bool vec, const TopkParams& p, hipStream_t s)
-{
-    return vec ? launch_topk_r<DT, true>(p, s) : launch_topk_r<DT, false>(p, s);
-}
-
 template <typename DT>
 hipError_t launch_absmax_t(bool vec, const TopkParams& p, hipStream_t s)
 {
@@ -103,11 +58,13 @@ hipError_t launch_key_absmax(int dtype, bool vec, const TopkParams& p, hipStream
     return launch_absmax_t<float>(vec, p, s);
 }
 
+// the retrieval kernels of each input type are instantiated in a translation unit of their
+// own (wf_topk_bf16.hip, wf_topk_f16.hip, wf_topk_f32.hip), compiled in parallel
 hipError_t launch_causal_topk(int dtype, bool vec, const TopkParams& p, hipStream_t s)
 {
-    if (dtype == 2) return launch_topk_t<bf16_t>(vec, p, s);
-    if (dtype == 1) return launch_topk_t<_Float16>(vec, p, s);
-    return launch_topk_t<float>(vec, p, s);
+    if (dtype == 2) return launch_causal_topk_bf16(vec, p, s);
+    if (dtype == 1) return launch_causal_topk_f16(vec, p, s);
+    return launch_causal_topk_f32(vec, p, s);
 }
 
 }  // namespace wf

@@ -48,7 +48,7 @@ namespace {
 constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
 constexpr int kTopkWaves = WF_TOPK_WAVES;                  // waves per workgroup (split the keys)
 constexpr int kBins = 128;                             // pruning histogram bins per row
-constexpr int kPD = 4;                                 // key steps each wave keeps in flight
+constexpr int kPD = 4;                                 // key steps each wave keeps in flight (2 for R > 128)
 constexpr int kStepMax = 16 * kTopkWaves;                  // appends per row in one key step of every wave, at most
 // |MFMA score - exact score| <= 2 * n * 2^-24 * sum_d |q_d k_d| for n accumulated terms with
 // round-to-nearest in both (2^-23 per term with truncating adds); the bound used is 2^-20
@@ -466,42 +466,51 @@ __device__ void rescore_row(Entry* pool, int c, const float* q, const DT* kb, in
 {
     if constexpr (VEC) {   // R == RP: every chunk lies inside the row
         constexpr int NC = RP / 8;
-        constexpr int U4 = NC * (sizeof(DT) == 4 ? 2 : 1);   // 16-byte loads per key row
+        // chunks loaded at once: all of them up to R = 128, else groups of 16 (the chain then
+        // continues over the next group, so the dims are still summed in ascending order)
+        constexpr int NCG = NC < 16 ? NC : 16;
+        constexpr int U4 = NCG * (sizeof(DT) == 4 ? 2 : 1);   // 16-byte loads per key row and group
         // key rows in flight per lane: 2 for 16-bit keys at R = 32 (measured faster than 4:
         // the phase is bound by its VALU work, not by load round trips), else 16 / U4
         constexpr int NBR = U4 >= 16 ? 1 : (U4 == 4 ? 2 : 16 / U4);
         for (int e0 = 0; e0 < c; e0 += 16 * NBR) {
-            uint4 lo[NBR][NC], hi[NBR][NC];
+            const DT* krow[NBR];
 #pragma unroll
             for (int m = 0; m < NBR; ++m) {
                 const int e = e0 + u + 16 * m;
                 const uint32_t jr = pool[min(e, c - 1)].j;   // unconditional read: no LDS wait per entry
-                const uint32_t j = e < c ? jr : 0u;
-                const DT* krow = kb + int64_t(j) * kst;
-#pragma unroll
-                for (int cc = 0; cc < NC; ++cc) {
-                    lo[m][cc] = *reinterpret_cast<const uint4*>(krow + 8 * cc);
-                    if constexpr (sizeof(DT) == 4) hi[m][cc] = *reinterpret_cast<const uint4*>(krow + 8 * cc + 4);
-                    else hi[m][cc] = make_uint4(0, 0, 0, 0);
-                }
+                krow[m] = kb + int64_t(e < c ? jr : 0u) * kst;
             }
             float acc[NBR];
 #pragma unroll
             for (int m = 0; m < NBR; ++m) acc[m] = 0.0f;
 #pragma unroll
-            for (int cc = 0; cc < NC; ++cc) {
-                const float4 qa = *reinterpret_cast<const float4*>(q + 8 * cc);
-                const float4 qb = *reinterpret_cast<const float4*>(q + 8 * cc + 4);
+            for (int c0 = 0; c0 < NC; c0 += NCG) {
+                uint4 lo[NBR][NCG], hi[NBR][NCG];
 #pragma unroll
                 for (int m = 0; m < NBR; ++m) {
-                    float kf[8];
-                    to_f32x8<DT>(lo[m][cc], hi[m][cc], kf);
-                    float a = acc[m];
-                    a = fmaf(qa.x, kf[0], a); a = fmaf(qa.y, kf[1], a);
-                    a = fmaf(qa.z, kf[2], a); a = fmaf(qa.w, kf[3], a);
-                    a = fmaf(qb.x, kf[4], a); a = fmaf(qb.y, kf[5], a);
-                    a = fmaf(qb.z, kf[6], a); a = fmaf(qb.w, kf[7], a);
-                    acc[m] = a;
+#pragma unroll
+                    for (int cc = 0; cc < NCG; ++cc) {
+                        lo[m][cc] = *reinterpret_cast<const uint4*>(krow[m] + 8 * (c0 + cc));
+                        if constexpr (sizeof(DT) == 4) hi[m][cc] = *reinterpret_cast<const uint4*>(krow[m] + 8 * (c0 + cc) + 4);
+                        else hi[m][cc] = make_uint4(0, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int cc = 0; cc < NCG; ++cc) {
+                    const float4 qa = *reinterpret_cast<const float4*>(q + 8 * (c0 + cc));
+                    const float4 qb = *reinterpret_cast<const float4*>(q + 8 * (c0 + cc) + 4);
+#pragma unroll
+                    for (int m = 0; m < NBR; ++m) {
+                        float kf[8];
+                        to_f32x8<DT>(lo[m][cc], hi[m][cc], kf);
+                        float a = acc[m];
+                        a = fmaf(qa.x, kf[0], a); a = fmaf(qa.y, kf[1], a);
+                        a = fmaf(qa.z, kf[2], a); a = fmaf(qa.w, kf[3], a);
+                        a = fmaf(qb.x, kf[4], a); a = fmaf(qb.y, kf[5], a);
+                        a = fmaf(qb.z, kf[6], a); a = fmaf(qb.w, kf[7], a);
+                        acc[m] = a;
+                    }
                 }
             }
 #pragma unroll
@@ -768,6 +777,11 @@ __device__ void write_row(const uint64_t (&key)[KP2 / 16], int kept, int64_t row
     }
 }
 
+// The retrieval kernel variant of (RC, KP2): two workgroups per CU up to R = 64 and K = 256,
+// else one (the wide kernel: its LDS and registers exceed the two-per-CU budget).
+template <int RC, int KP2>
+constexpr bool kWideTopk = RC > 2 || KP2 > 256;
+
 // No stage after the retrieval (the retrieval kernels). A tail type with kActive = true runs
 // its run(...) once every row of the block has been emitted, with each emitted index row
 // (k_eff int32) at the start of that row's pool in LDS (the single-pass fused kernel).
@@ -781,7 +795,8 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
     constexpr int RP = RC * 32;
     // pool entries per row: two workgroups (<= 80 KiB of LDS each) per CU for RC <= 2; the
     // wide variant runs one workgroup per CU (register-bound) and has LDS to spare
-    constexpr int POOL = 512;
+    constexpr int POOL = KP2 > 256 ? 768 : 512;
+    constexpr int PD = RC >= 8 ? 2 : kPD;   // key steps in flight per wave (operand registers)
     // pool checks every CG key steps: every step for K > 128, whose pruned pools keep so many
     // entries that the room a check interval must reserve decides how often they are pruned
     // (config 5: 18.5 -> 11.3 prunes per block, 2.20 -> 2.04 ms), every 2 steps otherwise
@@ -790,7 +805,7 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
     constexpr int LIMIT = POOL - CG * kStepMax;  // a pool above this is pruned at the next check
     constexpr int HEADROOM = 64;                 // a prune must leave this much room
     static_assert(LIMIT - HEADROOM > KP2 + 32, "pool too small for K");
-    static_assert(sizeof(TopkSmem<RP, POOL>) <= (RC <= 2 ? 80 : 160) * 1024, "LDS per workgroup");
+    static_assert(sizeof(TopkSmem<RP, POOL>) <= (kWideTopk<RC, KP2> ? 160 : 80) * 1024, "LDS per workgroup");
     __shared__ TopkSmem<RP, POOL> sm;
 
     const int lane = lane_id();
@@ -953,24 +968,24 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
         budget = max(1, (POOL - cmax) / (CG * kStepMax));
     };
     if (iters > 0) {
-        uint4 blo[kPD][RC], bhi[kPD][RC];
+        uint4 blo[PD][RC], bhi[PD][RC];
         // issued in buffer order (the scheduler must not reorder them): the loop then waits
         // for the two oldest loads only
 #pragma unroll
-        for (int v = 0; v < kPD; ++v) {
+        for (int v = 0; v < PD; ++v) {
             load_step(16 * min(w + kTopkWaves * v, nfull - 1), blo[v], bhi[v]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        for (int it0 = 0; it0 < iters; it0 += kPD) {
+        for (int it0 = 0; it0 < iters; it0 += PD) {
 #pragma unroll
-            for (int h = 0; h < kPD; h += 2) {   // one 2-step unit
+            for (int h = 0; h < PD; h += 2) {   // one 2-step unit
                 // both MFMAs read their buffers before the refills overwrite them
                 const f32x4_t acc0 = score(blo[h], bhi[h]);
                 const f32x4_t acc1 = score(blo[h + 1], bhi[h + 1]);
                 const int st0 = w + kTopkWaves * (it0 + h);
                 const int st1 = st0 + kTopkWaves;
-                load_step(16 * min(st0 + kTopkWaves * kPD, nfull - 1), blo[h], bhi[h]);
-                load_step(16 * min(st1 + kTopkWaves * kPD, nfull - 1), blo[h + 1], bhi[h + 1]);
+                load_step(16 * min(st0 + kTopkWaves * PD, nfull - 1), blo[h], bhi[h]);
+                load_step(16 * min(st1 + kTopkWaves * PD, nfull - 1), blo[h + 1], bhi[h + 1]);
                 if (st0 < nfull) consider(acc0, st0 * 16 + 4 * g);
                 if constexpr (CG == 1) {
                     if (--budget == 0) check();

@@ -20,8 +20,8 @@ from routing_attention.kernels._common import has_hip, promote_compute_dtype
 METHODS = ("auto", "fused_causal", "triton", "tiled", "streaming", "brute_force")
 
 # Largest address dim (R) and k_eff the HIP kernel takes (include/wayfinder_hip.h).
-MAX_ADDRESS_DIM = 128
-MAX_TOP_K = 256
+MAX_ADDRESS_DIM = 256
+MAX_TOP_K = 512
 
 
 def causal_topk_available() -> bool:
