@@ -3,9 +3,11 @@ decoder are captured once with torch.cuda.graph and replayed several times, with
 inputs copied into the captured buffers and eager calls of the same path between the
 replays; every replay must equal the eager result bit for bit (both paths are
 deterministic: the retrieval writes indices in canonical order and the readout has no
-atomics). The readout backward (index transpose by its own radix passes, row and key
-passes) is captured the same way. Nothing on these paths issues a memset, so the captured
-graphs hold kernel nodes only."""
+atomics), and the fused replays are checked against the C oracle too (indices bit-exact,
+output within the bf16 tolerance), so a replay that repeated a stale result would fail. The
+readout backward (index transpose by its own radix passes, row and key passes) is captured
+the same way and its replays checked against the float64 gradient oracle. Nothing on these
+paths issues a memset, so the captured graphs hold kernel nodes only."""
 
 from __future__ import annotations
 
@@ -14,10 +16,12 @@ import sys
 import pytest
 import torch
 
+from oracle import native
+from oracle.readout_grad import grads_autograd
 from routing_attention.kernels import fused_sparse_attention
 from routing_attention.kernels.sparse_autograd import readout_bwd, readout_fwd_lse
 from routing_attention.models import TransformerLM
-from tests.helpers import addresses, qkv
+from tests.helpers import addresses, qkv, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -55,6 +59,11 @@ def test_fused_forward_graph_replays(device):
     def fwd():
         return fused_sparse_attention(*static[:2], *static[2:], K, scale)
 
+    refs = []
+    for src in inputs:
+        qa, ka, q, k, v = (t.cpu() for t in src)
+        ri = native.causal_topk(qa, ka, K)
+        refs.append((ri, native.sparse_readout(q, k, v, ri, scale)))
     g, (g_out, g_idx) = _capture(fwd)
     for rep in range(4):
         for s, src in zip(static, inputs[rep % 2]):
@@ -64,6 +73,9 @@ def test_fused_forward_graph_replays(device):
         torch.cuda.synchronize()
         assert torch.equal(g_idx, e_idx), f"replay {rep}: indices differ"
         assert torch.equal(g_out, e_out), f"replay {rep}: output differs"
+        ri, ro = refs[rep % 2]
+        assert torch.equal(g_idx.cpu(), ri), f"replay {rep}: indices differ from the oracle"
+        assert rel_err(g_out.float(), ro) < 2e-2, f"replay {rep}: output differs from the oracle"
     assert not torch.equal(inputs[0][0], inputs[1][0])
 
 
@@ -121,3 +133,7 @@ def test_readout_backward_graph_replays(device):
         torch.cuda.synchronize()
         for name, a, b in zip(("dq", "dk", "dv"), g_grads, e_grads):
             assert torch.equal(a, b), f"replay {rep}: {name} differs"
+        q, k, v, idx, _, dout = (t.cpu() for t in sets[rep % 2])
+        _, rq, rk, rv = grads_autograd(q, k, v, idx, scale, dout)
+        for name, a, r in zip(("dq", "dk", "dv"), g_grads, (rq, rk, rv)):
+            assert rel_err(a.float(), r) < 2e-2, f"replay {rep}: {name} differs from the oracle"
