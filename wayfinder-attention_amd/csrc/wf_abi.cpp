@@ -10,6 +10,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -95,6 +96,21 @@ int64_t gcd64(int64_t a, int64_t b)
     return a;
 }
 
+// Speculative screening threshold of the retrieval: each row block estimates, from a strided
+// sample of its key prefix, a threshold that about kSeedAlpha * k_eff keys of the prefix reach,
+// screens with it, and checks every row exactly afterwards (rows that fail are screened again
+// from -inf in the same workgroup). WAYFINDER_TOPK_SEED_ALPHA overrides it (0 turns the seed
+// off: every row then starts at -inf, as the reference's streaming top-K does).
+constexpr float kSeedAlpha = 3.0f;
+
+float seed_alpha()   // read at every launch: a caller may change it between calls
+{
+    const char* e = std::getenv("WAYFINDER_TOPK_SEED_ALPHA");
+    if (!e || !*e) return kSeedAlpha;
+    const float v = std::strtof(e, nullptr);
+    return v > 1.0f ? v : 0.0f;
+}
+
 constexpr int64_t kMaxTopK = 512;
 constexpr int64_t kMaxR = 256;
 constexpr int64_t kMaxD = 256;
@@ -154,6 +170,7 @@ bool topk_prepare(const void* query, const void* key, int dtype, int64_t B, int6
     p.rb_begin = 0;
     p.rb_end = p.n_row_blocks;
     p.n_cus = wf::device_cu_count();
+    p.seed_alpha = seed_alpha();
     // vector loads; key rows are addressed with 32-bit byte offsets from the batch base and
     // every 32-dim chunk the kernel reads lies inside the row (R = 32, 64, 128 or 256)
     return (R == 32 || R == 64 || R == 128 || R == 256) &&

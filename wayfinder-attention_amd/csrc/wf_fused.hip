@@ -65,7 +65,9 @@ struct AllHeadsReadout {
             const int s0 = (tt % nb) * NBT;
 #pragma unroll
             for (int u = 0; u < NBT; ++u) {
-                const int j = __builtin_amdgcn_readfirstlane(li[min(s0 + u, K - 1)]);   // in [0, T)
+                // in [0, T) from the retrieval; clamped as well, so a gather can never leave the keys
+                const uint32_t j = min(uint32_t(__builtin_amdgcn_readfirstlane(li[min(s0 + u, K - 1)])),
+                                       uint32_t(T - 1));
                 const char* kr = kb + uint64_t(j) * kst;
                 const char* vr = vb + uint64_t(j) * vst;
 #pragma unroll

@@ -109,6 +109,8 @@ struct TopkParams {
     int64_t n_row_blocks;    // ceil(T / 16)
     int64_t rb_begin, rb_end;  // row blocks [rb_begin, rb_end) of this launch
     int64_t n_cus;           // compute units of the device (dispatch order of the row blocks)
+    float seed_alpha;        // speculative screening threshold: ~seed_alpha * k_eff keys pass
+                             // it (0: off, every row starts at -inf)
 };
 
 struct ReadoutParams {

@@ -47,6 +47,7 @@ namespace {
 
 constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
 constexpr int kTopkWaves = WF_TOPK_WAVES;                  // waves per workgroup (split the keys)
+constexpr int kSeedSteps = 128;                        // sampled key steps of a seed, at most
 constexpr int kBins = 128;                             // pruning histogram bins per row
 constexpr int kPD = 4;                                 // key steps each wave keeps in flight (2 for R > 128)
 constexpr int kStepMax = 16 * kTopkWaves;                  // appends per row in one key step of every wave, at most
@@ -303,6 +304,8 @@ struct TopkSmem {
     int cnt[kRows];                // pool fill
     float thr[kRows];              // screening threshold (-inf until K candidates are known)
     float eps[kRows];              // |MFMA score - exact score| bound of the row
+    float seed[kRows];             // speculative screening threshold (-inf: none)
+    int fail[kRows];               // the row's seed was too high: screen it again from -inf
 };
 
 // Largest bin b (of the row's kBins-bin histogram) whose suffix count C(b) reaches `need`;
@@ -680,12 +683,33 @@ template <int KP2>
 __device__ void write_row(const uint64_t (&key)[KP2 / 16], int kept, int64_t row, int64_t T,
                           int64_t k_eff, int32_t* out_idx, float* out_scores, int32_t* lidx, int u);
 
+// Element i (row-uniform) of a row's sorted keys, in every lane of the row: element i sits
+// in lane i / EPL, register i % EPL.
+template <int EPL>
+__device__ __forceinline__ uint64_t row_element(const uint64_t (&key)[EPL], int i, int u)
+{
+    uint64_t v = 0;
+#pragma unroll
+    for (int m = 0; m < EPL; ++m) v = m == i % EPL ? key[m] : v;
+    return row_max16_u64(u == i / EPL ? v : 0ull);
+}
+
+// lidx if the row's k_eff-th key (0: fewer were kept) has a score >= lidx_min, else null
+__device__ __forceinline__ int32_t* lidx_gate(int32_t* lidx, uint64_t kth, float lidx_min)
+{
+    if (!lidx || lidx_min == -__builtin_inff()) return lidx;
+    return kth != 0ull && key_entry(kth).s >= lidx_min ? lidx : nullptr;
+}
+
 // Sort row r's (exactly scored) winners into canonical order and write them plus pads.
 // `row` is the query position t in its batch; out_idx/out_scores point at the batch; lidx,
 // if not null, receives a copy of the index row in LDS (the row's own pool, already read).
+// Returns the row's k_eff-th key in canonical order (0 if fewer than k_eff were kept); the
+// LDS copy goes to lidx only if that key's score reaches lidx_min.
 template <int KP2, int POOL>
-__device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
-                         int64_t k_eff, int32_t* out_idx, float* out_scores, int32_t* lidx, int u)
+__device__ uint64_t emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
+                             int64_t k_eff, int32_t* out_idx, float* out_scores, int32_t* lidx,
+                             float lidx_min, int u)
 {
     constexpr int EPL = KP2 / 16;   // elements per lane; element i = u * EPL + m
     uint64_t key[EPL];
@@ -696,7 +720,9 @@ __device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
         key[m] = i < kept ? make_key(__uint_as_float(en.x), en.y) : 0ull;
     }
     bitonic_sort<EPL, KP2>(key, u);
-    write_row<KP2>(key, kept, row, T, k_eff, out_idx, out_scores, lidx, u);
+    const uint64_t kth = row_element<EPL>(key, int(k_eff) - 1, u);
+    write_row<KP2>(key, kept, row, T, k_eff, out_idx, out_scores, lidx_gate(lidx, kth, lidx_min), u);
+    return kth;
 }
 
 // Exact selection fused into the sort, for K in (64, 128] and c <= 144 exactly scored
@@ -705,9 +731,12 @@ __device__ void emit_row(const Entry* pool, int kept, int64_t row, int64_t T,
 // C[i] = max(A[i], B[127 - i]) holds the 128 largest of A and B as a bitonic sequence
 // (A falls, the reversed B rises), and one bitonic merge sorts it. This replaces the radix
 // select's histogram rounds with a 16-element sort, one exchange and seven merge steps.
+// Returns the row's k_eff-th key in canonical order (0 if fewer than k_eff were kept); the
+// LDS copy goes to lidx only if that key's score reaches lidx_min.
 template <int POOL>
-__device__ void emit_row_merge(const Entry* pool, int c, int64_t row, int64_t T, int64_t k_eff,
-                               int32_t* out_idx, float* out_scores, int32_t* lidx, int u)
+__device__ uint64_t emit_row_merge(const Entry* pool, int c, int64_t row, int64_t T, int64_t k_eff,
+                                   int32_t* out_idx, float* out_scores, int32_t* lidx,
+                                   float lidx_min, int u)
 {
     constexpr int KP2 = 128, EPL = 8, NB = 16;
     static_assert(POOL >= KP2 + NB, "pool too small");
@@ -732,7 +761,10 @@ __device__ void emit_row_merge(const Entry* pool, int c, int64_t row, int64_t T,
         key[m] = o > key[m] ? o : key[m];
     }
     bitonic_merge<EPL, KP2>(key, u);
-    write_row<KP2>(key, c < KP2 ? c : KP2, row, T, k_eff, out_idx, out_scores, lidx, u);
+    const uint64_t kth = row_element<EPL>(key, int(k_eff) - 1, u);
+    write_row<KP2>(key, c < KP2 ? c : KP2, row, T, k_eff, out_idx, out_scores,
+                   lidx_gate(lidx, kth, lidx_min), u);
+    return kth;
 }
 
 // Write a row's sorted keys (the first `kept` are winners) and the pads after them; with
@@ -775,6 +807,41 @@ __device__ void write_row(const uint64_t (&key)[KP2 / 16], int kept, int64_t row
         oi[i] = j;
         if (lidx) lidx[i] = j;
     }
+}
+
+// Speculative seed of one row (16 lanes u): a value that at least rk of the row's m sampled
+// values (group maxima, at sv[0..m), m <= 16 NV) reach, found by bisection of [min, max] and
+// accepted once between rk and ~1.25 rk of them reach it. Any value is safe as a seed: the
+// row is checked exactly after its screen. Non-finite samples end the search early (the
+// check then fails, or the seed is -inf).
+template <int NV>
+__device__ float seed_select(const float* sv, int m, int rk, int u)
+{
+    float v[NV];
+    float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        v[i] = u + 16 * i < m ? sv[u + 16 * i] : -__builtin_inff();
+        if (u + 16 * i < m) { lo = fminf(lo, v[i]); hi = fmaxf(hi, v[i]); }
+    }
+    lo = row_min16(lo);
+    hi = row_max16(hi);
+    const int accept = rk + (rk >> 2) + 2;
+    for (int it = 0; it < 20; ++it) {   // every value reaches lo
+        const float mid = 0.5f * lo + 0.5f * hi;
+        if (!(mid > lo && mid < hi)) break;
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) c += int(v[i] >= mid);
+        c = row_sum16_i32(c);
+        if (c >= rk) {
+            lo = mid;
+            if (c <= accept) break;
+        } else {
+            hi = mid;
+        }
+    }
+    return lo;
 }
 
 // The retrieval kernel variant of (RC, KP2): two workgroups per CU up to R = 64 and K = 256,
@@ -856,6 +923,8 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
     if (threadIdx.x < kRows) {
         sm.cnt[threadIdx.x] = 0;
         sm.thr[threadIdx.x] = -__builtin_inff();
+        sm.seed[threadIdx.x] = -__builtin_inff();
+        sm.fail[threadIdx.x] = 0;
     }
     float mk = 0.0f;
     const int64_t nch = last / kAbsmaxChunk + 1;
@@ -872,14 +941,14 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
 #ifdef WF_TOPK_TIMING
     uint64_t tm0 = wall_clock64();
     uint64_t tcomp = 0, ncomp = 0;
+    uint64_t tm1 = 0, tmA = 0, tmB = 0;
+    int c_in = 0, c_pr = 0, npass = 0;
 #endif
     // ---- screen
     // Steps 0 .. nfull-1 hold keys below the block's first row r0, so they need neither a
     // causal mask nor clamping; step nfull (the diagonal, keys r0 .. r0+15) is taken once,
     // after the loop, by wave nfull % kTopkWaves. The loop keeps kPD key loads in flight per wave
     // in distinct registers (the unrolled v) and never waits for more than the oldest.
-    // rows past T never take candidates; their threshold is +inf
-    float th = row_ok ? -__builtin_inff() : __builtin_inff();
     const int Ti = int(T);
     const int rowi = int(row);
     const int r0i = int(r0);
@@ -905,182 +974,277 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
             }
         }
     };
-    // append the lane's candidates (keys jb .. jb+3 of row n) that reach the threshold; one
-    // LDS atomic reserves their slots, the others are written to a dummy slot of the row
-    // the row's pool and this lane's dummy slot as LDS pointers, formed once: an append then
-    // advances one pointer instead of recomputing a slot address per entry
-    Entry* const pool_row = sm.pool[n];
-    Entry* const pool_dummy = pool_row + POOL + g;
-    auto append = [&](const f32x4_t& acc, const bool (&pp)[4], int jb) {
-        const int cntp = int(pp[0]) + int(pp[1]) + int(pp[2]) + int(pp[3]);
-        Entry* dst = pool_row + atomicAdd(&sm.cnt[n], cntp);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *(pp[i] ? dst : pool_dummy) = Entry{acc[i], uint32_t(jb + i)};
-            dst += int(pp[i]);
-        }
-    };
-    auto consider = [&](const f32x4_t& acc, int jb) {
-        const bool pp[4] = {acc[0] >= th, acc[1] >= th, acc[2] >= th, acc[3] >= th};
-        if (pp[0] || pp[1] || pp[2] || pp[3]) append(acc, pp, jb);
-    };
     auto score = [&](const uint4 (&alo)[RC], const uint4 (&ahi)[RC]) {
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < RC; ++c) acc = mfma_chunk<DT>(alo[c], ahi[c], qlo[c], qhi[c], acc);
         return acc;
     };
-    // budget: check intervals (CG key steps) every wave may still take before a pool could
-    // overflow (a step of all waves appends at most kStepMax per row). Every wave must take
-    // the same decisions at a check (the barriers must pair up), so they all decide on one
-    // snapshot of the counts: a second barrier keeps every wave from appending again until
-    // all of them have read it.
-    int budget = max(1, (POOL - 0) / (CG * kStepMax));
-    auto check = [&]() {
-        __syncthreads();   // every append of the unit has landed
-        int cl = lane < kRows ? sm.cnt[lane] : 0;
-        __syncthreads();   // the snapshot is read in every wave before anyone appends again
-        if (__ballot(cl > LIMIT)) {
-#ifdef WF_TOPK_TIMING
-            const uint64_t tc0 = wall_clock64();
-#endif
-            const int c = rr < kRows ? sm.cnt[rr] : 0;
-            const int cw = wave_max_of_rows(c);
-            if (c > K) {
-                int c2 = c;
-                const bool ok = prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr],
-                                                  sm.thr[rr], sm.eps[rr], K, u);
-                if (!ok || c2 > LIMIT - HEADROOM)
-                    exact_row<DT, VEC, RP, POOL, false>(sm.pool[rr], sm.hist[rr], c2, POOL, sm.cnt[rr],
-                                                 sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
-                                                 p.ksr, R, K, u);
+
+    // ---- seed
+    // A row that starts at -inf appends every key until its pool first fills, and its
+    // threshold then climbs one prune at a time (~1000 appends and 3 prunes per row at config 4).
+    // Instead, the block scores ns strided 16-key steps of its full steps first and sets each
+    // row's threshold (the seed) where about seed_alpha * K keys of the prefix would reach it:
+    // the value that rk of the row's 4 ns group maxima (keys 4g..4g+3 of a step) reach, a
+    // group of 4 independent keys reaching it with probability 1 - (1 - pf)^4. The seed is a
+    // guess, and the selection stays exact by a check instead: a key the seed rejects has
+    // MFMA score < seed, hence exact score < seed + eps, so it cannot be among the row's K
+    // best when the row's K-th best exact score s_K0 is >= seed + eps. A row that fails the
+    // check keeps its pool and screens its prefix again (pass 1, same workgroup) for the keys
+    // the seed rejected that can still matter: MFMA score in [s_K0 - 2 eps, seed) when it
+    // kept K (any key of the K best has exact score >= s_K0, MFMA score >= s_K0 - eps), or
+    // below the seed when it kept fewer.
+    if (p.seed_alpha > 0.0f && nfull >= 16) {
+        const float pf = p.seed_alpha * float(K) / float(16 * nfull);   // block-uniform
+        if (pf < 0.5f) {
+            int ns = min(max(int(ceilf(1.25f / pf)), 16), kSeedSteps);   // ~16+ maxima above the seed
+            ns = min(ns, nfull);
+            ns -= ns % (kTopkWaves * 4);
+            const int per_w = ns / kTopkWaves;   // steps per wave, equal in every wave
+            float* const samp = reinterpret_cast<float*>(sm.pool[n]);   // group maxima of row n
+            for (int i0 = 0; i0 < per_w; i0 += PD) {
+                uint4 slo[PD][RC], shi[PD][RC];
+#pragma unroll
+                for (int v = 0; v < PD; ++v) {   // step j of the sample is full step j * nfull / ns
+                    const int j = w + kTopkWaves * min(i0 + v, per_w - 1);
+                    load_step(16 * int((int64_t(j) * nfull) / ns), slo[v], shi[v]);
+                }
+#pragma unroll
+                for (int v = 0; v < PD; ++v) {
+                    const f32x4_t a = score(slo[v], shi[v]);
+                    if (i0 + v < per_w)
+                        samp[4 * (w + kTopkWaves * (i0 + v)) + g] = fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+                }
             }
-            __syncthreads();   // every row is pruned
-            th = row_ok ? sm.thr[n] : __builtin_inff();
-            cl = lane < kRows ? sm.cnt[lane] : 0;
-            __syncthreads();   // ... and read everywhere before anyone appends again
+            __syncthreads();   // every group maximum is in LDS
+            const int m = 4 * ns;
+            const float q1 = (1.0f - pf) * (1.0f - pf);
+            const int rk = max(1, int((1.0f - q1 * q1) * float(m) + 0.5f));
+            const float* const sv = reinterpret_cast<const float*>(sm.pool[rr]);
+            const float sd = m <= 16 * 16 ? seed_select<16>(sv, m, rk, u) : seed_select<kSeedSteps / 4>(sv, m, rk, u);
+            if (u == 0) { sm.seed[rr] = sd; sm.thr[rr] = sd; }
+            __syncthreads();   // the seeds are set before any wave screens
+        }
+    }
 #ifdef WF_TOPK_TIMING
-            tcomp += wall_clock64() - tc0;
-            ++ncomp;
+    const uint64_t tmS = wall_clock64();
 #endif
-        }
-        const int cmax = __builtin_amdgcn_readfirstlane(row_max16_i32(cl));
-        budget = max(1, (POOL - cmax) / (CG * kStepMax));
-    };
-    if (iters > 0) {
-        uint4 blo[PD][RC], bhi[PD][RC];
-        // issued in buffer order (the scheduler must not reorder them): the loop then waits
-        // for the two oldest loads only
+
+    // one screen and finish; pass 1 (rows whose seed failed) is a second inlined copy, not a
+    // loop, which would keep every loop-invariant value of the finish alive through both screens
+    auto run_pass = [&](const int pass) __attribute__((always_inline)) {
+#ifdef WF_TOPK_TIMING
+        npass = pass + 1;
+#endif
+        // rows past T never take candidates; their threshold is +inf. Pass 1 takes the band
+        // [thr, seed) of the rows that failed their check (the others have thr = +inf).
+        float th = row_ok ? sm.thr[n] : __builtin_inff();
+        const float th_hi = pass == 1 ? sm.seed[n] : __builtin_inff();
+        // append the lane's candidates (keys jb .. jb+3 of row n) that reach the threshold; one
+        // LDS atomic reserves their slots, the others are written to a dummy slot of the row
+        // the row's pool and this lane's dummy slot as LDS pointers, formed once: an append then
+        // advances one pointer instead of recomputing a slot address per entry
+        Entry* const pool_row = sm.pool[n];
+        Entry* const pool_dummy = pool_row + POOL + g;
+        auto append = [&](const f32x4_t& acc, const bool (&pp)[4], int jb) {
+            const int cntp = int(pp[0]) + int(pp[1]) + int(pp[2]) + int(pp[3]);
+            Entry* dst = pool_row + atomicAdd(&sm.cnt[n], cntp);
 #pragma unroll
-        for (int v = 0; v < PD; ++v) {
-            load_step(16 * min(w + kTopkWaves * v, nfull - 1), blo[v], bhi[v]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        for (int it0 = 0; it0 < iters; it0 += PD) {
+            for (int i = 0; i < 4; ++i) {
+                *(pp[i] ? dst : pool_dummy) = Entry{acc[i], uint32_t(jb + i)};
+                dst += int(pp[i]);
+            }
+        };
+        auto consider = [&](const f32x4_t& acc, int jb) {
+            bool pp[4] = {acc[0] >= th, acc[1] >= th, acc[2] >= th, acc[3] >= th};
+            if (pass == 1) {
 #pragma unroll
-            for (int h = 0; h < PD; h += 2) {   // one 2-step unit
-                // both MFMAs read their buffers before the refills overwrite them
-                const f32x4_t acc0 = score(blo[h], bhi[h]);
-                const f32x4_t acc1 = score(blo[h + 1], bhi[h + 1]);
-                const int st0 = w + kTopkWaves * (it0 + h);
-                const int st1 = st0 + kTopkWaves;
-                load_step(16 * min(st0 + kTopkWaves * PD, nfull - 1), blo[h], bhi[h]);
-                load_step(16 * min(st1 + kTopkWaves * PD, nfull - 1), blo[h + 1], bhi[h + 1]);
-                if (st0 < nfull) consider(acc0, st0 * 16 + 4 * g);
-                if constexpr (CG == 1) {
+                for (int i = 0; i < 4; ++i) pp[i] = pp[i] && acc[i] < th_hi;
+            }
+            if (pp[0] || pp[1] || pp[2] || pp[3]) append(acc, pp, jb);
+        };
+        // budget: check intervals (CG key steps) every wave may still take before a pool could
+        // overflow (a step of all waves appends at most kStepMax per row). Every wave must take
+        // the same decisions at a check (the barriers must pair up), so they all decide on one
+        // snapshot of the counts: a second barrier keeps every wave from appending again until
+        // all of them have read it.
+        // (pass 1 starts from the pools pass 0 left: at most max(K, KP2 + 16) entries a row)
+        int budget = max(1, (POOL - (pass == 0 ? 0 : __builtin_amdgcn_readfirstlane(
+                                         row_max16_i32(lane < kRows ? sm.cnt[lane] : 0)))) / (CG * kStepMax));
+        auto check = [&]() {
+            __syncthreads();   // every append of the unit has landed
+            int cl = lane < kRows ? sm.cnt[lane] : 0;
+            __syncthreads();   // the snapshot is read in every wave before anyone appends again
+            if (__ballot(cl > LIMIT)) {
+#ifdef WF_TOPK_TIMING
+                const uint64_t tc0 = wall_clock64();
+#endif
+                const int c = rr < kRows ? sm.cnt[rr] : 0;
+                const int cw = wave_max_of_rows(c);
+                if (c > K) {
+                    int c2 = c;
+                    const bool ok = prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr],
+                                                      sm.thr[rr], sm.eps[rr], K, u);
+                    if (!ok || c2 > LIMIT - HEADROOM)
+                        exact_row<DT, VEC, RP, POOL, false>(sm.pool[rr], sm.hist[rr], c2, POOL, sm.cnt[rr],
+                                                     sm.thr[rr], sm.eps[rr], sm.q[rr], kb, p.kst,
+                                                     p.ksr, R, K, u);
+                }
+                __syncthreads();   // every row is pruned
+                // a prune's threshold may fall below the seed; in pass 0 the seed still holds
+                th = row_ok ? (pass == 0 ? fmaxf(sm.thr[n], sm.seed[n]) : sm.thr[n]) : __builtin_inff();
+                cl = lane < kRows ? sm.cnt[lane] : 0;
+                __syncthreads();   // ... and read everywhere before anyone appends again
+#ifdef WF_TOPK_TIMING
+                tcomp += wall_clock64() - tc0;
+                ++ncomp;
+#endif
+            }
+            const int cmax = __builtin_amdgcn_readfirstlane(row_max16_i32(cl));
+            budget = max(1, (POOL - cmax) / (CG * kStepMax));
+        };
+        if (iters > 0) {
+            uint4 blo[PD][RC], bhi[PD][RC];
+            // issued in buffer order (the scheduler must not reorder them): the loop then waits
+            // for the two oldest loads only
+#pragma unroll
+            for (int v = 0; v < PD; ++v) {
+                load_step(16 * min(w + kTopkWaves * v, nfull - 1), blo[v], bhi[v]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            for (int it0 = 0; it0 < iters; it0 += PD) {
+#pragma unroll
+                for (int h = 0; h < PD; h += 2) {   // one 2-step unit
+                    // both MFMAs read their buffers before the refills overwrite them
+                    const f32x4_t acc0 = score(blo[h], bhi[h]);
+                    const f32x4_t acc1 = score(blo[h + 1], bhi[h + 1]);
+                    const int st0 = w + kTopkWaves * (it0 + h);
+                    const int st1 = st0 + kTopkWaves;
+                    load_step(16 * min(st0 + kTopkWaves * PD, nfull - 1), blo[h], bhi[h]);
+                    load_step(16 * min(st1 + kTopkWaves * PD, nfull - 1), blo[h + 1], bhi[h + 1]);
+                    if (st0 < nfull) consider(acc0, st0 * 16 + 4 * g);
+                    if constexpr (CG == 1) {
+                        if (--budget == 0) check();
+                    }
+                    if (st1 < nfull) consider(acc1, st1 * 16 + 4 * g);
                     if (--budget == 0) check();
                 }
-                if (st1 < nfull) consider(acc1, st1 * 16 + 4 * g);
-                if (--budget == 0) check();
             }
         }
-    }
-    if (w == nfull % kTopkWaves) {   // the diagonal step: keys r0 .. r0+15, causal mask
-        uint4 alo[RC], ahi[RC];
-        if constexpr (VEC) {
-            // the block's last rows may pass T: clamp those lanes' key to T-1 (masked below)
-            const int j = min(r0i + n, Ti - 1);
+        if (w == nfull % kTopkWaves) {   // the diagonal step: keys r0 .. r0+15, causal mask
+            uint4 alo[RC], ahi[RC];
+            if constexpr (VEC) {
+                // the block's last rows may pass T: clamp those lanes' key to T-1 (masked below)
+                const int j = min(r0i + n, Ti - 1);
 #pragma unroll
-            for (int c = 0; c < RC; ++c) {
-                const uint32_t off = uint32_t(j) * krow + uint32_t(8 * g + 32 * c) * uint32_t(sizeof(DT));
-                alo[c] = *reinterpret_cast<const uint4*>(kbytes + off);
-                if constexpr (sizeof(DT) == 4) ahi[c] = *reinterpret_cast<const uint4*>(kbytes + off + 16u);
-                else ahi[c] = make_uint4(0, 0, 0, 0);
+                for (int c = 0; c < RC; ++c) {
+                    const uint32_t off = uint32_t(j) * krow + uint32_t(8 * g + 32 * c) * uint32_t(sizeof(DT));
+                    alo[c] = *reinterpret_cast<const uint4*>(kbytes + off);
+                    if constexpr (sizeof(DT) == 4) ahi[c] = *reinterpret_cast<const uint4*>(kbytes + off + 16u);
+                    else ahi[c] = make_uint4(0, 0, 0, 0);
+                }
+            } else {
+                load_step(r0i, alo, ahi);
             }
-        } else {
-            load_step(r0i, alo, ahi);
+            const f32x4_t acc = score(alo, ahi);
+            const int jb = r0i + 4 * g;
+            const bool pp[4] = {acc[0] >= th && acc[0] < th_hi && jb <= rowi,
+                                acc[1] >= th && acc[1] < th_hi && jb + 1 <= rowi,
+                                acc[2] >= th && acc[2] < th_hi && jb + 2 <= rowi,
+                                acc[3] >= th && acc[3] < th_hi && jb + 3 <= rowi};
+            if (pp[0] || pp[1] || pp[2] || pp[3]) append(acc, pp, jb);
         }
-        const f32x4_t acc = score(alo, ahi);
-        const int jb = r0i + 4 * g;
-        const bool pp[4] = {acc[0] >= th && jb <= rowi, acc[1] >= th && jb + 1 <= rowi,
-                            acc[2] >= th && jb + 2 <= rowi, acc[3] >= th && jb + 3 <= rowi};
-        if (pp[0] || pp[1] || pp[2] || pp[3]) append(acc, pp, jb);
-    }
-    // ---- finish: prune, rescore exactly, select, sort, write
-    __syncthreads();
+        // ---- finish: prune, rescore exactly, select, sort, write, check the seed
+        __syncthreads();
 #ifdef WF_TOPK_TIMING
-    uint64_t tm1 = wall_clock64();
+        tm1 = wall_clock64();
 #endif
+        // pass 1 finishes only the rows it screened again
+        const bool row_live = rr < kRows && r0 + rr < T && (pass == 0 || sm.fail[rr] != 0);
+        int c = row_live ? sm.cnt[rr] : 0;   // rows past T hold 0 in every lane
 #ifdef WF_TOPK_TIMING
-    uint64_t tmA = 0, tmB = 0;
-    int c_in = 0, c_pr = 0;
+        c_in = c;
 #endif
-    const bool row_live = rr < kRows && r0 + rr < T;
-    int c = row_live ? sm.cnt[rr] : 0;   // rows past T hold 0 in every lane
+        const int cw = wave_max_of_rows(c);
+        if (row_live && c > K) {
+            int c2 = c;
+            prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
+            c = c2;
+        }
 #ifdef WF_TOPK_TIMING
-    c_in = c;
+        tmA = wall_clock64();
+        c_pr = c;
 #endif
-    const int cw = wave_max_of_rows(c);
-    if (row_live && c > K) {
-        int c2 = c;
-        prune_sized<(KP2 <= 128), POOL>(sm.pool[rr], sm.hist[rr], c, cw, c2, sm.cnt[rr], sm.thr[rr], sm.eps[rr], K, u);
-        c = c2;
-    }
+        const int cw2 = wave_max_of_rows(c);   // counts after the prune, every lane of the wave
+        if (row_live) {
+            int32_t* const oidx = p.out_idx + b * T * p.k_eff;
 #ifdef WF_TOPK_TIMING
-    tmA = wall_clock64();
-    c_pr = c;
-#endif
-    const int cw2 = wave_max_of_rows(c);   // counts after the prune, every lane of the wave
-    if (row_live) {
-        int32_t* const oidx = p.out_idx + b * T * p.k_eff;
-#ifdef WF_TOPK_TIMING
-        float* const oscr = nullptr;   // out_scores carries the timestamps
+            float* const oscr = nullptr;   // out_scores carries the timestamps
 #else
-        float* const oscr = p.out_scores ? p.out_scores + b * T * p.k_eff : nullptr;
+            float* const oscr = p.out_scores ? p.out_scores + b * T * p.k_eff : nullptr;
 #endif
-        int32_t* const lidx = Tail::kActive ? reinterpret_cast<int32_t*>(sm.pool[rr]) : nullptr;
-        bool done = false;
-        if constexpr (KP2 == 128) {
-            if (cw2 <= KP2 + 16) {   // wave-uniform: selection fused into the sort
-                rescore_row<DT, VEC, RP>(sm.pool[rr], c, sm.q[rr], kb, p.kst, p.ksr, R, u);
+            // a seeded row's pool must outlive a failed check: its index row reaches LDS after it
+            const float sd = sm.seed[rr];
+            const bool checked = pass == 0 && sd > -__builtin_inff();
+            int32_t* const lidx = Tail::kActive ? reinterpret_cast<int32_t*>(sm.pool[rr]) : nullptr;
+            const float lidx_min = checked ? sd + sm.eps[rr] : -__builtin_inff();
+            bool done = false;
+            uint64_t kth = 0;   // the row's K-th best key (exact score), 0 if it kept fewer
+            if constexpr (KP2 == 128) {
+                if (cw2 <= KP2 + 16) {   // wave-uniform: selection fused into the sort
+                    rescore_row<DT, VEC, RP>(sm.pool[rr], c, sm.q[rr], kb, p.kst, p.ksr, R, u);
+#ifdef WF_TOPK_TIMING
+                    tmB = wall_clock64();
+#endif
+                    kth = emit_row_merge<POOL>(sm.pool[rr], c, r0 + rr, T, p.k_eff, oidx, oscr, lidx, lidx_min, u);
+                    done = true;
+                }
+            }
+            if (!done) {
+                const int kept = exact_row<DT, VEC, RP, POOL, (KP2 <= 128)>(sm.pool[rr], sm.hist[rr], c, cw2,
+                                                                           sm.cnt[rr], sm.thr[rr], sm.eps[rr],
+                                                                           sm.q[rr], kb, p.kst, p.ksr, R, K, u);
 #ifdef WF_TOPK_TIMING
                 tmB = wall_clock64();
 #endif
-                emit_row_merge<POOL>(sm.pool[rr], c, r0 + rr, T, p.k_eff, oidx, oscr, lidx, u);
-                done = true;
+                kth = emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, oidx, oscr, lidx, lidx_min, u);
+            }
+            if (checked) {
+                const float eps = sm.eps[rr];
+                const bool good = kth != 0ull && key_entry(kth).s >= sd + eps;
+                if (!good && u == 0) {
+                    sm.fail[rr] = 1;
+                    sm.thr[rr] = kth != 0ull ? key_entry(kth).s - 2.0f * eps : -__builtin_inff();
+                }
             }
         }
-        if (!done) {
-            const int kept = exact_row<DT, VEC, RP, POOL, (KP2 <= 128)>(sm.pool[rr], sm.hist[rr], c, cw2,
-                                                                       sm.cnt[rr], sm.thr[rr], sm.eps[rr],
-                                                                       sm.q[rr], kb, p.kst, p.ksr, R, K, u);
-#ifdef WF_TOPK_TIMING
-            tmB = wall_clock64();
-#endif
-            emit_row<KP2, POOL>(sm.pool[rr], kept, r0 + rr, T, p.k_eff, oidx, oscr, lidx, u);
+    };
+    run_pass(0);
+    __syncthreads();   // every row's check is done
+    const int fl = lane < kRows ? sm.fail[lane] : 0;
+    if (__ballot(fl != 0)) {   // the same flags in every wave
+        __syncthreads();   // ... read everywhere before the reset
+        // rows that passed are final: they take nothing more, and with count 0 no check prunes
+        // them (the single-pass kernel keeps their index rows at the start of their pools)
+        if (threadIdx.x < kRows && !sm.fail[threadIdx.x]) {
+            sm.thr[threadIdx.x] = __builtin_inff();
+            sm.cnt[threadIdx.x] = 0;
         }
+        __syncthreads();
+        run_pass(1);
     }
     if constexpr (Tail::kActive) {
         __syncthreads();   // every row's index list is in LDS
         tail.run(reinterpret_cast<const char*>(sm.pool), sizeof(sm.pool[0]), b, r0, T, K, w, lane);
     }
 #ifdef WF_TOPK_TIMING
-    const uint64_t tmC = wall_clock64();
     __syncthreads();
     if (threadIdx.x == 0 && p.out_scores) {
         uint64_t* tm = reinterpret_cast<uint64_t*>(p.out_scores) + 8 * blockIdx.x;
         tm[0] = tm0; tm[1] = tm1; tm[2] = wall_clock64(); tm[3] = uint64_t(rb) | (ncomp << 16) | (tcomp << 32);
-        tm[4] = tmA; tm[5] = tmB; tm[6] = tmC; tm[7] = uint64_t(c_in) | (uint64_t(c_pr) << 32);
+        tm[4] = tmA; tm[5] = tmB; tm[6] = tmS;
+        tm[7] = uint64_t(c_in) | (uint64_t(npass) << 24) | (uint64_t(c_pr) << 32);
     }
 #endif
 }
