@@ -93,6 +93,21 @@ def test_seeded_topk_matches_oracle(device, alpha, kind, a, B, T, R, K, dtype, n
         assert idx[0, -1].tolist() == list(range(K))
 
 
+@pytest.mark.parametrize("T,lo,hi,K", [(8192, 5000, 5600, 128), (16384, 9000, 10200, 64), (12000, 2000, 2600, 100)])
+def test_burst_overflows_stretched_checks(device, alpha, T, lo, hi, K):
+    """A run of keys aligned with every query: nearly all of them pass the seed within one
+    stretched check interval, so pools overflow (appends stay inside the pool, the count
+    shows it) and those rows are screened again from -inf with worst-case checks."""
+    _say(f"[seed] burst keys {lo}..{hi} of T={T}, K={K}")
+    alpha(None)
+    B, R = 1, 32
+    qa, ka = addresses(B, T, R, seed=T + lo, dtype=torch.float32)
+    mu = torch.ones(R) / R ** 0.5
+    qa = qa + 0.5 * mu
+    ka[:, lo:hi] = ka[:, lo:hi] + 1.5 * mu
+    _check(qa.to(torch.bfloat16), ka.to(torch.bfloat16), K, device)
+
+
 def test_seeded_topk_repeatable_across_alphas(device, alpha):
     """The seed changes the work, never the result: the same indices at every alpha."""
     _say("[seed] identical indices at alpha 0, 1.01, 2, default")

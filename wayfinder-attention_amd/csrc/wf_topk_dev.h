@@ -48,6 +48,7 @@ namespace {
 constexpr int kRows = 16;                              // query rows per workgroup (MFMA N)
 constexpr int kTopkWaves = WF_TOPK_WAVES;                  // waves per workgroup (split the keys)
 constexpr int kSeedSteps = 128;                        // sampled key steps of a seed, at most
+constexpr int kMaxStretch = 8;                         // pool check interval of a seeded pass 0, at most x
 constexpr int kBins = 128;                             // pruning histogram bins per row
 constexpr int kPD = 4;                                 // key steps each wave keeps in flight (2 for R > 128)
 constexpr int kStepMax = 16 * kTopkWaves;                  // appends per row in one key step of every wave, at most
@@ -995,9 +996,17 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
     // the seed rejected that can still matter: MFMA score in [s_K0 - 2 eps, seed) when it
     // kept K (any key of the K best has exact score >= s_K0, MFMA score >= s_K0 - eps), or
     // below the seed when it kept fewer.
+    // Pool checks of a seeded block in pass 0 come `stretch` times less often than the worst
+    // case (every key of every wave reaching the threshold) requires: about pf of the keys
+    // reach a seed, so an interval stretched by 1 / (4 pf) takes a quarter of the room it
+    // reserves, on average. A pool that still overflows (clamped appends keep every write in
+    // the pool) is detected by its count, and its row is screened again from -inf in pass 1,
+    // whose checks reserve the worst case.
+    int stretch = 1;
     if (p.seed_alpha > 0.0f && nfull >= 16) {
         const float pf = p.seed_alpha * float(K) / float(16 * nfull);   // block-uniform
         if (pf < 0.5f) {
+            stretch = max(1, min(kMaxStretch, int(0.25f / pf)));
             int ns = min(max(int(ceilf(1.25f / pf)), 16), kSeedSteps);   // ~16+ maxima above the seed
             ns = min(ns, nfull);
             ns -= ns % (kTopkWaves * 4);
@@ -1049,7 +1058,8 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
         Entry* const pool_dummy = pool_row + POOL + g;
         auto append = [&](const f32x4_t& acc, const bool (&pp)[4], int jb) {
             const int cntp = int(pp[0]) + int(pp[1]) + int(pp[2]) + int(pp[3]);
-            Entry* dst = pool_row + atomicAdd(&sm.cnt[n], cntp);
+            // slot + cntp <= POOL unless a stretched interval overflowed the pool
+            Entry* dst = pool_row + min(atomicAdd(&sm.cnt[n], cntp), POOL - cntp);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 *(pp[i] ? dst : pool_dummy) = Entry{acc[i], uint32_t(jb + i)};
@@ -1070,17 +1080,19 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
         // snapshot of the counts: a second barrier keeps every wave from appending again until
         // all of them have read it.
         // (pass 1 starts from the pools pass 0 left: at most max(K, KP2 + 16) entries a row)
-        int budget = max(1, (POOL - (pass == 0 ? 0 : __builtin_amdgcn_readfirstlane(
+        const int bmul = pass == 0 ? stretch : 1;
+        int budget = bmul * max(1, (POOL - (pass == 0 ? 0 : __builtin_amdgcn_readfirstlane(
                                          row_max16_i32(lane < kRows ? sm.cnt[lane] : 0)))) / (CG * kStepMax));
         auto check = [&]() {
             __syncthreads();   // every append of the unit has landed
             int cl = lane < kRows ? sm.cnt[lane] : 0;
+            if (cl > POOL) sm.fail[lane] = 2;   // overflowed: screen the row again from -inf
             __syncthreads();   // the snapshot is read in every wave before anyone appends again
             if (__ballot(cl > LIMIT)) {
 #ifdef WF_TOPK_TIMING
                 const uint64_t tc0 = wall_clock64();
 #endif
-                const int c = rr < kRows ? sm.cnt[rr] : 0;
+                const int c = rr < kRows ? min(sm.cnt[rr], POOL) : 0;
                 const int cw = wave_max_of_rows(c);
                 if (c > K) {
                     int c2 = c;
@@ -1102,7 +1114,7 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
 #endif
             }
             const int cmax = __builtin_amdgcn_readfirstlane(row_max16_i32(cl));
-            budget = max(1, (POOL - cmax) / (CG * kStepMax));
+            budget = bmul * max(1, (POOL - cmax) / (CG * kStepMax));
         };
         if (iters > 0) {
             uint4 blo[PD][RC], bhi[PD][RC];
@@ -1160,9 +1172,12 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
 #ifdef WF_TOPK_TIMING
         tm1 = wall_clock64();
 #endif
-        // pass 1 finishes only the rows it screened again
-        const bool row_live = rr < kRows && r0 + rr < T && (pass == 0 || sm.fail[rr] != 0);
-        int c = row_live ? sm.cnt[rr] : 0;   // rows past T hold 0 in every lane
+        // pass 1 finishes only the rows it screened again; pass 0 leaves overflowed rows to it
+        const int craw = rr < kRows && r0 + rr < T ? sm.cnt[rr] : 0;
+        const bool ovf = pass == 0 && (craw > POOL || sm.fail[rr] == 2);
+        if (ovf && u == 0) sm.fail[rr] = 2;
+        const bool row_live = rr < kRows && r0 + rr < T && !ovf && (pass == 0 || sm.fail[rr] != 0);
+        int c = row_live ? craw : 0;   // rows past T hold 0 in every lane
 #ifdef WF_TOPK_TIMING
         c_in = c;
 #endif
@@ -1226,10 +1241,13 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
     if (__ballot(fl != 0)) {   // the same flags in every wave
         __syncthreads();   // ... read everywhere before the reset
         // rows that passed are final: they take nothing more, and with count 0 no check prunes
-        // them (the single-pass kernel keeps their index rows at the start of their pools)
-        if (threadIdx.x < kRows && !sm.fail[threadIdx.x]) {
-            sm.thr[threadIdx.x] = __builtin_inff();
-            sm.cnt[threadIdx.x] = 0;
+        // them (the single-pass kernel keeps their index rows at the start of their pools);
+        // overflowed rows start again from an empty pool and take every key
+        if (threadIdx.x < kRows) {
+            const int f = sm.fail[threadIdx.x];
+            if (f != 1) sm.cnt[threadIdx.x] = 0;
+            if (f == 0) sm.thr[threadIdx.x] = __builtin_inff();
+            if (f == 2) { sm.thr[threadIdx.x] = -__builtin_inff(); sm.seed[threadIdx.x] = __builtin_inff(); }
         }
         __syncthreads();
         run_pass(1);
@@ -1244,7 +1262,9 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
         uint64_t* tm = reinterpret_cast<uint64_t*>(p.out_scores) + 8 * blockIdx.x;
         tm[0] = tm0; tm[1] = tm1; tm[2] = wall_clock64(); tm[3] = uint64_t(rb) | (ncomp << 16) | (tcomp << 32);
         tm[4] = tmA; tm[5] = tmB; tm[6] = tmS;
-        tm[7] = uint64_t(c_in) | (uint64_t(npass) << 24) | (uint64_t(c_pr) << 32);
+        int novf = 0;   // rows whose pool overflowed in pass 0
+        for (int r = 0; r < kRows; ++r) novf += sm.fail[r] == 2;
+        tm[7] = uint64_t(c_in) | (uint64_t(npass) << 24) | (uint64_t(min(novf, 15)) << 28) | (uint64_t(c_pr) << 32);
     }
 #endif
 }
