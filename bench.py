@@ -383,7 +383,8 @@ def main():
     ms_topk = time_loop(lambda: causal_topk(dev["qa"], dev["ka"], K), args.steps, 3)
     ms_read = time_loop(lambda: sparse_meat_attention(dev["q"], dev["k"], dev["v"], idx, scale),
                         args.steps, 3)
-    ms_probe = time_loop(gather_probe_fn(dev, idx), args.steps, 3)
+    # the probe reproduces the 16-bit readout's loads; fp32 inputs (config 1) have none
+    ms_probe = time_loop(gather_probe_fn(dev, idx), args.steps, 3) if dtype != torch.float32 else None
     k_eff = min(K, T)
     gathered = 2 * B * H * T * k_eff * D * s
     score_flops = B * R * T * (T + 1)
@@ -426,7 +427,7 @@ def main():
         "pipelined_ms_per_call": round(ms, 4),
         "rows_per_s": round(B * T / (ms * 1e-3), 1),
         "kernels_ms": {"causal_topk": round(ms_topk, 4), "sparse_readout": round(ms_read, 4),
-                       "gather_probe": round(ms_probe, 4)},
+                       "gather_probe": round(ms_probe, 4) if ms_probe else None},
         # dominant kernel: the readout. achieved = its HBM bytes per launch (rocprofv3
         # FETCH_SIZE + WRITE_SIZE, calibrated on a device copy) / its HIP-event time
         "roofline": {"bound": "hbm", "kernel": "sparse_readout_fast",
@@ -438,7 +439,8 @@ def main():
                      # the same loads with no arithmetic
                      "gather_path": {"probe_ms": round(ms_probe, 4), "readout_ms": round(ms_read, 4),
                                      "frac": round(ms_probe / ms_read, 4),
-                                     "probe_gathered_gbs": round(gathered / (ms_probe * 1e-3) / 1e9, 1)},
+                                     "probe_gathered_gbs": round(gathered / (ms_probe * 1e-3) / 1e9, 1)}
+                                    if ms_probe else None,
                      # SURVEY 8(d)'s count: one K and one V row per (query, head, neighbour)
                      "algorithmic_gather_inclusive": {
                          "bytes": readout_bytes,
