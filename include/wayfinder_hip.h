@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define WF_ABI_VERSION 3
+#define WF_ABI_VERSION 4
 
 typedef enum wf_status {
     WF_OK = 0,
@@ -175,6 +175,36 @@ size_t wf_sparse_readout_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, in
  * B*T*K < 2^32.
  */
 int wf_sparse_readout_bwd(const wf_readout_bwd_args* args, void* stream);
+
+/*
+ * Training forward of the readout with dropout on the attention weights.
+ * Replaces: the reference's non-fused training readout (routing_attention/models/attention.py:
+ *           35-55): attn = dropout(softmax(scale q.k_s)); out = sum_s attn_s v_s.
+ * Weight s of row t of head h in batch b is kept with probability 1 - dropout_p and scaled
+ * by 1 / (1 - dropout_p). The keep decision is a counter-based hash of (seed, b, h, t, s):
+ *   key  = mix(mix(lo32(r) ^ lo32(seed)) ^ hi32(r) ^ hi32(seed)),  r = (b*H + h)*T + t,
+ *   keep = mix(key ^ s) >= round(dropout_p * 2^32),
+ * with mix the "lowbias32" integer hash (x ^= x >> 16; x *= 0x7feb352d; x ^= x >> 15;
+ * x *= 0x846ca68b; x ^= x >> 16). The same seed gives the same mask, so the backward (below)
+ * recomputes it instead of storing it. lse2 (required) is the log-sum-exp of the undropped
+ * weights, as wf_sparse_readout_fwd_lse writes it. dropout_p in [0, 1): 0 is the plain
+ * training forward. Other arguments and limits as wf_sparse_readout_fwd_lse.
+ */
+int wf_sparse_readout_fwd_dropout(const void* q, const void* k, const void* v, int dtype,
+                                  int64_t B, int64_t H, int64_t T, int64_t D,
+                                  const int64_t* q_strides, const int64_t* k_strides,
+                                  const int64_t* v_strides,
+                                  const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                                  float scale, unsigned flags, float dropout_p, uint64_t seed,
+                                  void* out, const int64_t* out_strides, float* lse2, void* stream);
+
+/*
+ * Backward of wf_sparse_readout_fwd_dropout (same dropout_p and seed, hence the same mask m):
+ * as wf_sparse_readout_bwd with dp_s = m_s / (1 - dropout_p) * (dout . v_s) and
+ * dv_j = sum p_s m_s / (1 - dropout_p) dout_t. Arguments and limits as wf_sparse_readout_bwd.
+ */
+int wf_sparse_readout_bwd_dropout(const wf_readout_bwd_args* args, float dropout_p, uint64_t seed,
+                                  void* stream);
 
 /*
  * Learned-address projection and L2 normalisation, both address streams in one pass.

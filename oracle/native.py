@@ -45,6 +45,12 @@ def lib() -> ctypes.CDLL:
         l.wfo_sparse_readout.restype = None
         l.wfo_sparse_readout.argtypes = [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
                                          _i64, ctypes.c_float, ctypes.c_uint, _ptr]
+        l.wfo_sparse_readout_dropout.restype = None
+        l.wfo_sparse_readout_dropout.argtypes = [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
+                                                 _i64, ctypes.c_float, ctypes.c_uint,
+                                                 ctypes.c_float, ctypes.c_uint64, _ptr]
+        l.wfo_dropout_mask.restype = None
+        l.wfo_dropout_mask.argtypes = [_i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_uint64, _ptr]
         l.wfo_sparse_readout_rows.restype = None
         l.wfo_sparse_readout_rows.argtypes = [_ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr,
                                               _i64, _ptr, _i64, ctypes.c_float, ctypes.c_uint,
@@ -129,6 +135,26 @@ def sparse_readout(q, k, v, indices, scale: float, flags: int = 0) -> torch.Tens
     lib().wfo_sparse_readout(_p(qn), _p(kn), _p(vn), B, H, T, D, _p(idx), K,
                              float(scale), int(flags), _p(out))
     return torch.from_numpy(out)
+
+
+def sparse_readout_dropout(q, k, v, indices, scale: float, dropout_p: float, seed: int,
+                           flags: int = 0) -> torch.Tensor:
+    """The readout with dropout on the attention weights (hash mask of seed), float64."""
+    qn, kn, vn = _f32(q), _f32(k), _f32(v)
+    B, H, T, D = qn.shape
+    idx = np.ascontiguousarray(indices.detach().cpu().to(torch.int32).numpy(), dtype=np.int32)
+    K = idx.shape[-1]
+    out = np.empty((B, H, T, D), dtype=np.float64)
+    lib().wfo_sparse_readout_dropout(_p(qn), _p(kn), _p(vn), B, H, T, D, _p(idx), K, float(scale),
+                                     int(flags), float(dropout_p), int(seed) & (2 ** 64 - 1), _p(out))
+    return torch.from_numpy(out)
+
+
+def dropout_mask(B: int, H: int, T: int, K: int, dropout_p: float, seed: int) -> torch.Tensor:
+    """(B, H, T, K) bool keep mask of the readout's dropout for this seed."""
+    out = np.empty((B, H, T, K), dtype=np.uint8)
+    lib().wfo_dropout_mask(B, H, T, K, float(dropout_p), int(seed) & (2 ** 64 - 1), _p(out))
+    return torch.from_numpy(out).bool()
 
 
 def sparse_readout_rows(q, k, v, rows_bt, indices, scale: float, flags: int = 0) -> torch.Tensor:

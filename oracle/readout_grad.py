@@ -4,7 +4,8 @@ TEST INFRASTRUCTURE ONLY (imported by tests/, never by the product).
 
 * ``grads_autograd``: float64 autograd of the reference's differentiable readout,
   routing_attention/models/attention.py:35-55 with _gather_kv_heads :58-69 (gather k/v at
-  the shared indices, scores * scale, softmax, weighted sum of v), no dropout. Pinned by
+  the shared indices, scores * scale, softmax, weighted sum of v), optionally with a given
+  dropout mask on the weights. Pinned by
   ``torch.autograd.gradcheck`` (finite differences) in tests/test_oracle_grad.py.
 * ``dq_rows`` / ``dkdv_keys``: the closed-form gradients evaluated for a subset of query
   rows or key rows in float64, for spot checks at sizes where the (B, H, T, K, D) gathers of
@@ -35,8 +36,10 @@ def _pad_mask(T: int, K: int) -> torch.Tensor:
     return (t < K - 1) & (s > t)
 
 
-def grads_autograd(q, k, v, indices, scale, dout, mask_pads=False):
-    """(out, dq, dk, dv) in float64 for (B, H, T, D) q/k/v/dout and (B, T, K) indices."""
+def grads_autograd(q, k, v, indices, scale, dout, mask_pads=False, keep=None, drop_scale=1.0):
+    """(out, dq, dk, dv) in float64 for (B, H, T, D) q/k/v/dout and (B, T, K) indices.
+    ``keep`` (B, H, T, K) bool: dropout after the softmax (the reference's
+    ``attn = dropout(softmax(...))`` with this mask), kept weights times ``drop_scale``."""
     q, k, v = (t.detach().cpu().double().requires_grad_(True) for t in (q, k, v))
     B, H, T, D = q.shape
     j = _norm_idx(indices.cpu(), T)
@@ -49,6 +52,8 @@ def grads_autograd(q, k, v, indices, scale, dout, mask_pads=False):
     if mask_pads:
         scores = scores.masked_fill(_pad_mask(T, K).view(1, 1, T, K), float("-inf"))
     p = torch.softmax(scores, dim=-1)
+    if keep is not None:
+        p = p * keep.double() * float(drop_scale)
     out = (p.unsqueeze(-1) * v_sel).sum(dim=3)
     out.backward(dout.detach().cpu().double())
     return out.detach(), q.grad, k.grad, v.grad

@@ -25,6 +25,11 @@
  *      across heads :64-77, scores = (q . k_sel) * scale, softmax, weighted sum of v_sel),
  *    accumulated in double. Negative indices wrap by +T (torch advanced indexing);
  *    indices outside [-T, T) are clamped to [0, T-1] (the reference raises there).
+ *  - wfo_sparse_readout_dropout / wfo_dropout_mask: the reference's non-fused training
+ *    readout, routing_attention/models/attention.py:35-55 (attn = dropout(softmax(...))),
+ *    with the keep mask defined by a hash of (seed, b, h, t, s) -- the definition of
+ *    wf_sparse_readout_fwd_dropout in include/wayfinder_hip.h, restated here; the reference
+ *    draws its mask from torch's generator instead, which no implementation reproduces.
  *
  * Build: oracle/Makefile -> oracle/libwf_oracle.so (gcc, OpenMP over rows).
  */
@@ -162,17 +167,57 @@ void wfo_causal_topk(const float* qa, const float* ka, int64_t B, int64_t T, int
                              out_score ? out_score + b * T * k_eff : NULL);
 }
 
+/* Dropout keep decision (include/wayfinder_hip.h, wf_sparse_readout_fwd_dropout): the
+ * "lowbias32" integer hash (C. Wellons, hash-prospector) chained over the row id
+ * r = (b*H + h)*T + t and the seed halves, then over the slot s. */
+static uint32_t mix32(uint32_t x)
+{
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+static uint32_t drop_threshold(float p)
+{
+    const double t = floor((double)p * 4294967296.0 + 0.5);
+    return t > 4294967295.0 ? 0xffffffffu : (uint32_t)t;
+}
+
+static int drop_keep(uint64_t seed, uint64_t row_id, uint32_t slot, uint32_t thresh)
+{
+    const uint32_t key = mix32(mix32((uint32_t)row_id ^ (uint32_t)seed) ^ (uint32_t)(row_id >> 32) ^
+                               (uint32_t)(seed >> 32));
+    return mix32(key ^ slot) >= thresh;
+}
+
+/* out: contiguous (B, H, T, K) bytes, 1 = kept. */
+void wfo_dropout_mask(int64_t B, int64_t H, int64_t T, int64_t K, float p, uint64_t seed,
+                      uint8_t* out)
+{
+    const uint32_t thresh = drop_threshold(p);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < B * H * T; ++r)
+        for (int64_t s = 0; s < K; ++s) out[r * K + s] = (uint8_t)drop_keep(seed, (uint64_t)r, (uint32_t)s, thresh);
+}
+
 /*
  * One (b, h, t) row of the readout: softmax over the K slots of idx_row of
  * scale * q[b,h,t] . k[b,h,j], weighted sum of v[b,h,j], accumulated in double.
  * q, k, v: contiguous (B, H, T, D) fp32. sc / jj: scratch of K entries.
  * flags bit 0: zero weight for slots s > t of rows t < K - 1 (pad slots of the retrieval).
+ * drop_p > 0: after the softmax, weight s is kept if drop_keep(...) and scaled by
+ * 1 / (1 - drop_p) (computed in fp32, as the kernels do), else zeroed.
  */
 static void readout_row(const float* q, const float* k, const float* v, int64_t H, int64_t T,
                         int64_t D, int64_t b, int64_t h, int64_t t, const int32_t* idx_row,
-                        int64_t K, float scale, unsigned flags, double* sc, int64_t* jj,
-                        double* orow)
+                        int64_t K, float scale, unsigned flags, float drop_p, uint64_t seed,
+                        double* sc, int64_t* jj, double* orow)
 {
+    const uint32_t thresh = drop_threshold(drop_p);
+    const double dscale = (double)(1.0f / (1.0f - drop_p));
     const int64_t bh = b * H + h;
     const float* qr = q + (bh * T + t) * D;
     double m = -INFINITY;
@@ -196,8 +241,11 @@ static void readout_row(const float* q, const float* k, const float* v, int64_t 
         if (sc[s] == -INFINITY) continue;
         const double p = exp(sc[s] - m);
         l += p;
+        double w = p;
+        if (drop_p > 0.0f)
+            w = drop_keep(seed, (uint64_t)(bh * T + t), (uint32_t)s, thresh) ? p * dscale : 0.0;
         const float* vr = v + (bh * T + jj[s]) * D;
-        for (int64_t d = 0; d < D; ++d) orow[d] += p * (double)vr[d];
+        for (int64_t d = 0; d < D; ++d) orow[d] += w * (double)vr[d];
     }
     for (int64_t d = 0; d < D; ++d) orow[d] = l > 0.0 ? orow[d] / l : 0.0;
 }
@@ -206,10 +254,10 @@ static void readout_row(const float* q, const float* k, const float* v, int64_t 
  * q, k, v: contiguous (B, H, T, D) fp32; idx: contiguous (B, T, K) int32;
  * out: contiguous (B, H, T, D) double (readout_row for every row).
  */
-void wfo_sparse_readout(const float* q, const float* k, const float* v,
-                        int64_t B, int64_t H, int64_t T, int64_t D,
-                        const int32_t* idx, int64_t K, float scale, unsigned flags,
-                        double* out)
+void wfo_sparse_readout_dropout(const float* q, const float* k, const float* v,
+                                int64_t B, int64_t H, int64_t T, int64_t D,
+                                const int32_t* idx, int64_t K, float scale, unsigned flags,
+                                float drop_p, uint64_t seed, double* out)
 {
 #pragma omp parallel
     {
@@ -220,12 +268,21 @@ void wfo_sparse_readout(const float* q, const float* k, const float* v,
             for (int64_t t = 0; t < T; ++t) {
                 const int64_t b = bh / H, h = bh % H;
                 readout_row(q, k, v, H, T, D, b, h, t, idx + (b * T + t) * K, K, scale, flags,
-                            sc, jj, out + (bh * T + t) * D);
+                            drop_p, seed, sc, jj, out + (bh * T + t) * D);
             }
         }
         free(sc);
         free(jj);
     }
+}
+
+/* wfo_sparse_readout_dropout without dropout. */
+void wfo_sparse_readout(const float* q, const float* k, const float* v,
+                        int64_t B, int64_t H, int64_t T, int64_t D,
+                        const int32_t* idx, int64_t K, float scale, unsigned flags,
+                        double* out)
+{
+    wfo_sparse_readout_dropout(q, k, v, B, H, T, D, idx, K, scale, flags, 0.0f, 0, out);
 }
 
 /*
@@ -246,7 +303,7 @@ void wfo_sparse_readout_rows(const float* q, const float* k, const float* v,
         for (int64_t i = 0; i < n; ++i) {
             for (int64_t h = 0; h < H; ++h)
                 readout_row(q, k, v, H, T, D, rows_bt[2 * i], h, rows_bt[2 * i + 1], idx + i * K,
-                            K, scale, flags, sc, jj, out + (i * H + h) * D);
+                            K, scale, flags, 0.0f, 0, sc, jj, out + (i * H + h) * D);
         }
         free(sc);
         free(jj);

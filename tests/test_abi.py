@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.wf_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.wf_abi_version() == _lib.ABI_VERSION == 4
 
 
 def _i64(*v):
@@ -195,6 +195,24 @@ def test_readout_bwd_contract_errors(lib, kw, code, msg):
 def test_readout_bwd_empty_is_noop(lib):
     assert _bwd(lib, T=0) == _lib.WF_OK
     assert _bwd(lib, B=0) == _lib.WF_OK
+
+
+@pytest.mark.parametrize("p", [-0.1, 1.0, 1.5, float("nan")])
+def test_dropout_probability_contract(lib, p):
+    st = _i64(2 * 64 * 64, 64, 128, 1)
+    rc = lib.wf_sparse_readout_fwd_dropout(FAKE, FAKE, FAKE, 2, 1, 2, 64, 64, st, st, st, FAKE,
+                                           _i64(64 * 8, 8, 1), 8, 0.125, 0, p, 1, FAKE, st, FAKE, None)
+    assert rc == _lib.WF_ERR_INVALID_ARGUMENT and "dropout_p" in _lib.last_error()
+    a = _lib.ReadoutBwdArgs()
+    assert lib.wf_sparse_readout_bwd_dropout(ctypes.byref(a), p, 1, None) == _lib.WF_ERR_INVALID_ARGUMENT
+    assert "dropout_p" in _lib.last_error()
+
+
+def test_dropout_forward_needs_lse(lib):
+    st = _i64(2 * 64 * 64, 64, 128, 1)
+    rc = lib.wf_sparse_readout_fwd_dropout(FAKE, FAKE, FAKE, 2, 1, 2, 64, 64, st, st, st, FAKE,
+                                           _i64(64 * 8, 8, 1), 8, 0.125, 0, 0.1, 1, FAKE, st, None, None)
+    assert rc == _lib.WF_ERR_INVALID_ARGUMENT and "lse2" in _lib.last_error()
 
 
 def test_readout_fwd_lse_needs_lse(lib):

@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -247,10 +248,24 @@ bool readout_prepare(const void* q, const void* k, const void* v, int dtype, int
     return readout_rows(p, 0, T);
 }
 
+// Dropout parameters for probability p (0 < p < 1) and a 64-bit seed: keep iff hash >= thresh,
+// thresh = round(p * 2^32), so P(keep) = 1 - thresh / 2^32.
+wf::DropoutParams make_dropout(float prob, uint64_t seed)
+{
+    wf::DropoutParams d{};
+    const double t = std::floor(double(prob) * 4294967296.0 + 0.5);
+    d.thresh = uint32_t(std::min(t, 4294967295.0));
+    d.k0 = uint32_t(seed);
+    d.k1 = uint32_t(seed >> 32);
+    d.scale = 1.0f / (1.0f - prob);
+    return d;
+}
+
 int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
                 int64_t T, int64_t D, const int64_t* qs, const int64_t* ks, const int64_t* vs,
                 const int32_t* idx, const int64_t* is, int64_t K, float scale, unsigned flags,
-                void* out, const int64_t* os, float* lse2, hipStream_t stream)
+                void* out, const int64_t* os, float* lse2, hipStream_t stream,
+                const wf::DropoutParams* drop = nullptr)
 {
     if (B * H * T == 0) return WF_OK;
     wf::ReadoutParams p;
@@ -258,6 +273,10 @@ int run_readout(const void* q, const void* k, const void* v, int dtype, int64_t 
     if (!readout_prepare(q, k, v, dtype, B, H, T, D, qs, ks, vs, idx, is, K, scale, flags, out, os,
                          lse2, p, &vec, &fast))
         return fail(WF_ERR_UNSUPPORTED, "sparse_readout: problem too large for one launch");
+    if (drop) {
+        p.drop_on = 1;
+        p.drop = *drop;
+    }
     const hipError_t e = wf::launch_sparse_readout(dtype, vec, fast, p, stream);
     if (e != hipSuccess) return hip_fail("sparse_readout: kernel launch", e);
     return WF_OK;
@@ -369,6 +388,68 @@ int fused_run(const wf_fused_args* a, void* ws, size_t ws_bytes, hipStream_t s)
     return WF_OK;
 }
 
+int readout_bwd(const wf_readout_bwd_args* a, const wf::DropoutParams* drop, void* stream)
+{
+    if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: NULL argument struct");
+    int rc = check_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
+                           a->k_strides, a->v_strides, a->indices, a->idx_strides, a->K, a->dout,
+                           a->dout_strides);
+    if (rc != WF_OK) return rc;
+    const int64_t B = a->B, H = a->H, T = a->T, D = a->D, K = a->K;
+    if (B * H * T == 0) return ok();
+    if (!a->dq || !a->dk || !a->dv || !a->lse2)
+        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: NULL dq/dk/dv/lse2 pointer");
+    if (B * T * K >= (int64_t(1) << 32) - 1 || B * T >= (int64_t(1) << 32) - 1)
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: B*T*K=%lld exceeds 32-bit list offsets", (long long)(B * T * K));
+    const int dt = a->dtype;
+    const int64_t es = int64_t(elem_size(dt));
+    auto fast_ok = [&](const void* base, const int64_t* st) {
+        return vec_ok(base, dt, st, 4, D) && st[2] >= 0 && (T - 1) * st[2] * es + D * es < (int64_t(1) << 32);
+    };
+    if (!(fast_ok(a->q, a->q_strides) && fast_ok(a->k, a->k_strides) && fast_ok(a->v, a->v_strides) &&
+          fast_ok(a->dout, a->dout_strides) && fast_ok(a->dq, a->dq_strides) &&
+          fast_ok(a->dk, a->dk_strides) && fast_ok(a->dv, a->dv_strides)))
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: every (B,H,T,D) tensor needs a contiguous head dim, "
+                                        "16-byte aligned rows and a per-(b,h) span below 4 GiB");
+    if (a->idx_strides[2] != 1)
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: index rows must be contiguous (idx_strides[2] == 1)");
+    const size_t need = wf::sparse_readout_bwd_workspace(B, H, T, K);
+    if (!a->workspace || a->workspace_bytes < need)
+        return fail(WF_ERR_WORKSPACE, "sparse_readout_bwd: workspace of %zu bytes required, got %zu", need,
+                    a->workspace ? a->workspace_bytes : size_t(0));
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0)
+        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: workspace not 256-byte aligned");
+    wf::ReadoutBwdParams p{};
+    p.q = a->q; p.k = a->k; p.v = a->v; p.dout = a->dout;
+    p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
+    p.idx = a->indices; p.lse2 = a->lse2;
+    for (int i = 0; i < 4; ++i) {
+        p.qs[i] = a->q_strides[i]; p.ks[i] = a->k_strides[i]; p.vs[i] = a->v_strides[i];
+        p.gs[i] = a->dout_strides[i]; p.dqs[i] = a->dq_strides[i]; p.dks[i] = a->dk_strides[i];
+        p.dvs[i] = a->dv_strides[i];
+    }
+    for (int i = 0; i < 3; ++i) p.is[i] = a->idx_strides[i];
+    p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
+    p.scale = a->scale; p.flags = a->flags & WF_FLAG_MASK_PADS;
+    const int64_t nbh = B * H;
+    p.row_begin = 0;
+    p.row_end = T;
+    p.seg_per_pair = 8 / gcd64(nbh, 8);
+    p.rows_per_seg = cdiv(T, p.seg_per_pair);
+    p.vpairs = nbh * p.seg_per_pair;
+    p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
+    if (p.vpairs * p.wg_per_vpair >= (int64_t(1) << 31))
+        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: problem too large for one launch");
+    if (drop) {
+        p.drop_on = 1;
+        p.drop = *drop;
+    }
+    const hipError_t e = wf::launch_sparse_readout_bwd(dt, p, a->workspace, a->workspace_bytes,
+                                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("sparse_readout_bwd: launch", e);
+    return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -435,68 +516,44 @@ int wf_sparse_readout_fwd_lse(const void* q, const void* k, const void* v, int d
     return rc == WF_OK ? ok() : rc;
 }
 
+int wf_sparse_readout_fwd_dropout(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                                  int64_t H, int64_t T, int64_t D, const int64_t* q_strides,
+                                  const int64_t* k_strides, const int64_t* v_strides,
+                                  const int32_t* indices, const int64_t* idx_strides, int64_t K,
+                                  float scale, unsigned flags, float dropout_p, uint64_t seed,
+                                  void* out, const int64_t* out_strides, float* lse2, void* stream)
+{
+    int rc = check_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
+                           idx_strides, K, out, out_strides);
+    if (rc != WF_OK) return rc;
+    if (!(dropout_p >= 0.0f && dropout_p < 1.0f))
+        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_fwd_dropout: dropout_p=%g not in [0, 1)", double(dropout_p));
+    if (!lse2 && B * H * T > 0) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_fwd_dropout: NULL lse2");
+    const wf::DropoutParams d = make_dropout(dropout_p, seed);
+    rc = run_readout(q, k, v, dtype, B, H, T, D, q_strides, k_strides, v_strides, indices,
+                     idx_strides, K, scale, flags & WF_FLAG_MASK_PADS, out, out_strides, lse2,
+                     static_cast<hipStream_t>(stream), dropout_p > 0.0f ? &d : nullptr);
+    return rc == WF_OK ? ok() : rc;
+}
+
 size_t wf_sparse_readout_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K)
 {
     if (B <= 0 || H <= 0 || T <= 0 || K <= 0) return 0;
     return wf::sparse_readout_bwd_workspace(B, H, T, K);
 }
 
+
 int wf_sparse_readout_bwd(const wf_readout_bwd_args* a, void* stream)
 {
-    if (!a) return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: NULL argument struct");
-    int rc = check_readout(a->q, a->k, a->v, a->dtype, a->B, a->H, a->T, a->D, a->q_strides,
-                           a->k_strides, a->v_strides, a->indices, a->idx_strides, a->K, a->dout,
-                           a->dout_strides);
-    if (rc != WF_OK) return rc;
-    const int64_t B = a->B, H = a->H, T = a->T, D = a->D, K = a->K;
-    if (B * H * T == 0) return ok();
-    if (!a->dq || !a->dk || !a->dv || !a->lse2)
-        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: NULL dq/dk/dv/lse2 pointer");
-    if (B * T * K >= (int64_t(1) << 32) - 1 || B * T >= (int64_t(1) << 32) - 1)
-        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: B*T*K=%lld exceeds 32-bit list offsets", (long long)(B * T * K));
-    const int dt = a->dtype;
-    const int64_t es = int64_t(elem_size(dt));
-    auto fast_ok = [&](const void* base, const int64_t* st) {
-        return vec_ok(base, dt, st, 4, D) && st[2] >= 0 && (T - 1) * st[2] * es + D * es < (int64_t(1) << 32);
-    };
-    if (!(fast_ok(a->q, a->q_strides) && fast_ok(a->k, a->k_strides) && fast_ok(a->v, a->v_strides) &&
-          fast_ok(a->dout, a->dout_strides) && fast_ok(a->dq, a->dq_strides) &&
-          fast_ok(a->dk, a->dk_strides) && fast_ok(a->dv, a->dv_strides)))
-        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: every (B,H,T,D) tensor needs a contiguous head dim, "
-                                        "16-byte aligned rows and a per-(b,h) span below 4 GiB");
-    if (a->idx_strides[2] != 1)
-        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: index rows must be contiguous (idx_strides[2] == 1)");
-    const size_t need = wf::sparse_readout_bwd_workspace(B, H, T, K);
-    if (!a->workspace || a->workspace_bytes < need)
-        return fail(WF_ERR_WORKSPACE, "sparse_readout_bwd: workspace of %zu bytes required, got %zu", need,
-                    a->workspace ? a->workspace_bytes : size_t(0));
-    if (reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0)
-        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd: workspace not 256-byte aligned");
-    wf::ReadoutBwdParams p{};
-    p.q = a->q; p.k = a->k; p.v = a->v; p.dout = a->dout;
-    p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
-    p.idx = a->indices; p.lse2 = a->lse2;
-    for (int i = 0; i < 4; ++i) {
-        p.qs[i] = a->q_strides[i]; p.ks[i] = a->k_strides[i]; p.vs[i] = a->v_strides[i];
-        p.gs[i] = a->dout_strides[i]; p.dqs[i] = a->dq_strides[i]; p.dks[i] = a->dk_strides[i];
-        p.dvs[i] = a->dv_strides[i];
-    }
-    for (int i = 0; i < 3; ++i) p.is[i] = a->idx_strides[i];
-    p.B = B; p.H = H; p.T = T; p.D = D; p.K = K;
-    p.scale = a->scale; p.flags = a->flags & WF_FLAG_MASK_PADS;
-    const int64_t nbh = B * H;
-    p.row_begin = 0;
-    p.row_end = T;
-    p.seg_per_pair = 8 / gcd64(nbh, 8);
-    p.rows_per_seg = cdiv(T, p.seg_per_pair);
-    p.vpairs = nbh * p.seg_per_pair;
-    p.wg_per_vpair = cdiv(p.rows_per_seg, wf::kReadoutRowsPerWG);
-    if (p.vpairs * p.wg_per_vpair >= (int64_t(1) << 31))
-        return fail(WF_ERR_UNSUPPORTED, "sparse_readout_bwd: problem too large for one launch");
-    const hipError_t e = wf::launch_sparse_readout_bwd(dt, p, a->workspace, a->workspace_bytes,
-                                                       static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_fail("sparse_readout_bwd: launch", e);
-    return ok();
+    return readout_bwd(a, nullptr, stream);
+}
+
+int wf_sparse_readout_bwd_dropout(const wf_readout_bwd_args* a, float dropout_p, uint64_t seed, void* stream)
+{
+    if (!(dropout_p >= 0.0f && dropout_p < 1.0f))
+        return fail(WF_ERR_INVALID_ARGUMENT, "sparse_readout_bwd_dropout: dropout_p=%g not in [0, 1)", double(dropout_p));
+    const wf::DropoutParams d = make_dropout(dropout_p, seed);
+    return readout_bwd(a, dropout_p > 0.0f ? &d : nullptr, stream);
 }
 
 int wf_address_project_fwd(const void* x, int dtype, int64_t B, int64_t T, int64_t d_model,

@@ -113,6 +113,60 @@ struct TopkParams {
                              // it (0: off, every row starts at -inf)
 };
 
+// Unsigned 32-bit division by a divisor fixed per launch (Granlund-Montgomery, round-up
+// multiplier): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, and for every 32-bit x
+// x / d = (t + ((x - t) >> 1)) >> (l - 1) with t = umulhi(x, m); d = 1 is the identity.
+struct FastDiv {
+    uint32_t m, l;
+};
+
+inline FastDiv make_fastdiv(uint32_t d)
+{
+    FastDiv f{0, 0};
+    if (d <= 1) return f;
+    while ((uint64_t(1) << f.l) < d) ++f.l;
+    f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << f.l) - d)) / d + 1);
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f)
+{
+    if (f.l == 0) return x;
+    const uint32_t t = __umulhi(x, f.m);
+    return (t + ((x - t) >> 1)) >> (f.l - 1);
+}
+
+// Dropout on the readout's attention weights. Slot s of query row t of head h in batch b is
+// kept when keep_hash(row_key(k, ((b*H + h)*T + t)), s) >= thresh, a Bernoulli(1 - p) draw for
+// thresh = round(p * 2^32); kept weights are scaled by 1 / (1 - p). The hash is the "lowbias32"
+// integer mixer (C. Wellons, hash-prospector, public domain) chained over the 64-bit row id and
+// the two halves of the 64-bit seed, then once more over the slot; the CPU oracle restates it.
+struct DropoutParams {
+    uint32_t thresh;   // keep iff hash >= thresh
+    uint32_t k0, k1;   // low and high words of the seed
+    float scale;       // 1 / (1 - p)
+};
+
+__host__ __device__ __forceinline__ uint32_t drop_mix32(uint32_t x)
+{
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+__host__ __device__ __forceinline__ uint32_t drop_row_key(const DropoutParams& d, uint64_t row_id)
+{
+    return drop_mix32(drop_mix32(uint32_t(row_id) ^ d.k0) ^ uint32_t(row_id >> 32) ^ d.k1);
+}
+
+__host__ __device__ __forceinline__ bool drop_keep(const DropoutParams& d, uint32_t row_key, uint32_t slot)
+{
+    return drop_mix32(row_key ^ slot) >= d.thresh;
+}
+
 struct ReadoutParams {
     const void* q;
     const void* k;
@@ -134,6 +188,8 @@ struct ReadoutParams {
     int head_major;         // workgroup order: 1 = virtual pair by virtual pair (grids larger
                             // than one residency wave), 0 = pair blockIdx % 8 (one wave);
                             // set by the launcher from the kernel's occupancy
+    int drop_on;            // dropout on the attention weights (then lse2 is set)
+    DropoutParams drop;
 };
 
 // Readout stage of the single-pass fused kernel (wf_fused.hip): the block's rows for all
@@ -166,7 +222,7 @@ struct ReadoutBwdParams {
     float2* row_stats;       // (B, H, T) workspace, row pass -> key pass: (lse2, delta) with
                              // delta = sum_s p_s (dout . v_s); one 8-byte load per list entry
     const uint32_t* off;     // (B*T + 1) start of each key's list in `rows`
-    const uint32_t* rows;    // query rows t referencing each key, grouped by key, t ascending
+    const uint32_t* rows;    // slots t*K + s referencing each key, grouped by key, t ascending
     int64_t qs[4], ks[4], vs[4], gs[4], dqs[4], dks[4], dvs[4];  // element strides (B, H, T, D)
     int64_t is[3];
     int64_t B, H, T, D, K;
@@ -174,6 +230,9 @@ struct ReadoutBwdParams {
     unsigned flags;
     int64_t row_begin, row_end;                                 // as in ReadoutParams
     int64_t seg_per_pair, rows_per_seg, vpairs, wg_per_vpair;
+    FastDiv divK;            // t = slot / K in the key pass
+    int drop_on;             // dropout on the attention weights, as in the forward
+    DropoutParams drop;
 };
 
 // Learned-address projection + normalisation (wf_address.hip).

@@ -53,9 +53,10 @@ struct Stage {
 // D: the lane layout's head dim (32, 64, 128, 256); the problem's p.D is any value up to D
 // (lanes holding dims past p.D read zeros and store nothing; a slice the head dim ends in is
 // read and written element by element). NB: wave steps per task.
-template <typename DT, bool VEC, int D, int NB>
+template <typename DT, bool VEC, int D, int NB, bool DROP = false>
 __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutParams p)
 {
+    static_assert(!DROP || NB <= D / 8, "dropout: one keep bit per lane");
     constexpr int LPN = D / 8;       // lanes per neighbour
     constexpr int NPS = 64 / LPN;    // neighbours per wave step
     constexpr int CH = NB * NPS;     // neighbour slots per task
@@ -131,6 +132,7 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
     uint4 qlo = make_uint4(0, 0, 0, 0), qhi = qlo;
     float m = -__builtin_inff(), l = 0.0f;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t rkey = 0;   // dropout: the row's hash key
 
     auto compute = [&](int tau, const Stage<NB>& st, const uint4 (&klo)[NB], const uint4 (&khi)[NB],
                        const uint4 (&vlo)[NB], const uint4 (&vhi)[NB]) {
@@ -142,7 +144,14 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
             l = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+            if (DROP) rkey = drop_row_key(p.drop, uint64_t(b * p.H + h) * uint64_t(T) + uint64_t(tw + tau / nb));
         }
+        // dropout keep bits of the group's slots bat*CH + u*NPS + grp: lane sub < NB hashes
+        // step sub's slot and one ballot hands every group its bits
+        uint32_t kbits = 0;
+        if (DROP)
+            kbits = uint32_t(__ballot(sub < NB && drop_keep(p.drop, rkey, uint32_t(bat * CH + sub * NPS + grp))) >>
+                             (grp * LPN));
         float sc[NB];
         float bm = -__builtin_inff();
 #pragma unroll
@@ -160,11 +169,12 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             const float pu = st.ok[u] ? exp2f(sc[u] - mn) : 0.0f;
-            l += pu;
+            l += pu;   // the normaliser counts every weight; dropout scales the values
+            const float wu = DROP ? ((kbits >> u) & 1u ? pu * p.drop.scale : 0.0f) : pu;
             float vf[8];
             cvt8<DT>(vlo[u], vhi[u], vf);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = fmaf(pu, vf[e], acc[e]);
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(wu, vf[e], acc[e]);
         }
         m = mn;
         if (bat == nb - 1) {
@@ -230,10 +240,11 @@ __global__ __launch_bounds__(64 * kWaves) void sparse_readout_kernel(ReadoutPara
 // multiple of 8 up to D. Lanes past p.D / 8 load the row's last slice (so no load is
 // conditional), zero their query slice (so they add nothing to any dot product) and store
 // nothing.
-template <typename DT, int D, int NB, bool LSE, bool TRUST, bool VI>
+template <typename DT, int D, int NB, bool LSE, bool TRUST, bool VI, bool DROP = false>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(sizeof(DT) == 2 && !LSE ? 4 : 1)))
 void sparse_readout_fast(ReadoutParams p)
 {
+    static_assert(!DROP || (LSE && NB <= D / 8), "dropout: training forward, one keep bit per lane");
     static_assert(NB % 2 == 0, "steps are consumed in pairs");
     static_assert(!VI || NB == 4, "one 16-byte index load per task");
     constexpr int LPN = D / 8;
@@ -303,6 +314,8 @@ void sparse_readout_fast(ReadoutParams p)
     float m = -__builtin_inff(), l = 0.0f;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int rc = 0, qc = 0;   // task being computed
+    uint32_t rkey = 0;    // dropout: the row's hash key
+    const uint64_t row_id0 = uint64_t(b * p.H + h) * uint64_t(T) + uint64_t(tw);
 
     // the query slices of the wave's rows, loaded once ahead of the pipeline and parked in
     // LDS (otherwise unused here) rather than in registers
@@ -326,10 +339,17 @@ void sparse_readout_fast(ReadoutParams p)
             l = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+            if (DROP) rkey = drop_row_key(p.drop, row_id0 + uint64_t(rc));
         }
         const int t = int(tw) + rc;
         const int slot0 = qc * CH + (VI ? grp * NB : grp);   // slot of step u: slot0 + u * SU
         constexpr int SU = VI ? 1 : NPS;
+        // dropout keep bits of the group's NB slots: lane sub < NB hashes slot0 + sub * SU and
+        // one ballot hands every group its bits
+        uint32_t kbits = 0;
+        if (DROP)
+            kbits = uint32_t(__ballot(sub < NB && drop_keep(p.drop, rkey, uint32_t(slot0 + sub * SU))) >>
+                             (grp * LPN));
         const int lim = (mask_flag && t < K - 1) ? t + 1 : K;   // slots >= lim carry no weight
         float sc[NB];
         float bm = -__builtin_inff();
@@ -360,8 +380,14 @@ void sparse_readout_fast(ReadoutParams p)
         for (int u = 0; u < NB; u += 2) {
             const float pa = __builtin_amdgcn_exp2f(sc[u] - ms);
             const float pc = __builtin_amdgcn_exp2f(sc[u + 1] - ms);
-            l += pa + pc;
-            pv2<DT>(acc, pa, pc, vlo[u], vhi[u], vlo[u + 1], vhi[u + 1]);
+            l += pa + pc;   // the normaliser counts every weight; dropout scales the values
+            if (DROP) {
+                const float wa = (kbits >> u) & 1u ? pa * p.drop.scale : 0.0f;
+                const float wc = (kbits >> (u + 1)) & 1u ? pc * p.drop.scale : 0.0f;
+                pv2<DT>(acc, wa, wc, vlo[u], vhi[u], vlo[u + 1], vhi[u + 1]);
+            } else {
+                pv2<DT>(acc, pa, pc, vlo[u], vhi[u], vlo[u + 1], vhi[u + 1]);
+            }
         }
         m = mn;
         if (qc == nb - 1) {
@@ -461,6 +487,10 @@ hipError_t launch_fast_d(const ReadoutParams& p, hipStream_t s)
     // aligned base and row strides that are multiples of 4)
     const bool vi = NB == 4 && p.K % 4 == 0 && p.K >= NB && reinterpret_cast<uintptr_t>(p.idx) % 16 == 0 &&
                     p.is[0] % 4 == 0 && p.is[1] % 4 == 0;
+    if (p.drop_on) {   // training forward with dropout (lse2 is set)
+        if (vi) return launch_readout<sparse_readout_fast<DT, D, NB, true, false, true, true>>(p, s);
+        return launch_readout<sparse_readout_fast<DT, D, NB, true, false, false, true>>(p, s);
+    }
     if (vi) {
         if (p.lse2) return launch_readout<sparse_readout_fast<DT, D, NB, true, false, true>>(p, s);
         if (p.flags & kFlagTrustedIndices) return launch_readout<sparse_readout_fast<DT, D, NB, false, true, true>>(p, s);
@@ -488,6 +518,7 @@ hipError_t launch_d(const ReadoutParams& p, hipStream_t s)
 #define WF_READOUT_NB 4
 #endif
     constexpr int NB = WF_READOUT_NB;
+    if (p.drop_on) return launch_readout<sparse_readout_kernel<DT, VEC, D, NB, true>>(p, s);
     return launch_readout<sparse_readout_kernel<DT, VEC, D, NB>>(p, s);
 }
 

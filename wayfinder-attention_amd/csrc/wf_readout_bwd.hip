@@ -10,10 +10,14 @@
 //   dk_j = scale * sum_{(t,s): j_s = j} p_s (dp_s - delta_t) q_t
 //   dv_j = sum_{(t,s): j_s = j} p_s dout_t
 //
+// With dropout on the weights (kept with mask m_s, scaled by c = 1/(1-p); the forward output
+// is sum_s p_s m_s c v_s) the same formulas hold with dp_s = m_s c (dout_t . v_{j_s}) and
+// dv_j = sum p_s m_s c dout_t; delta_t = sum_s p_s dp_s is still dout_t . out_t.
+//
 // computed without floating-point atomics, so the gradients are deterministic:
 //  1. index transpose: a stable LSD radix sort (8-bit digits; per pass a workgroup
 //     histogram, a per-digit scan over workgroups and a stable scatter ranked with wave
-//     ballots) of (b*T + j) keys with the query row t as value groups the rows that selected
+//     ballots) of (b*T + j) keys with the slot t*K + s as value groups the rows that selected
 //     each key, t ascending; a binary search per key over the sorted keys gives each list's
 //     offset. Masked pad slots sort past the last list. No memsets, no global atomics: every
 //     count is written whole, so the backward can be captured into a HIP graph.
@@ -36,32 +40,9 @@ constexpr int kSortItems = 16;                         // items per thread and p
 constexpr uint32_t kSortTile = kSortThreads * kSortItems;
 
 // Input of one radix pass: the (b, t, s) slots themselves on the first pass (key b*T + j with
-// j wrapped and clamped as in the forward, value t; masked pad slots -- s > t on rows
+// j wrapped and clamped as in the forward, value t*K + s; masked pad slots -- s > t on rows
 // t < K-1 with WF_FLAG_MASK_PADS -- get the key B*T, past every list), the previous pass's
 // arrays after it. B*T*K < 2^32 (checked by the entry point), so slot arithmetic is 32-bit.
-// Unsigned 32-bit division by a divisor fixed per launch (Granlund-Montgomery, round-up
-// multiplier): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, and for every 32-bit x
-// x / d = (t + ((x - t) >> 1)) >> (l - 1) with t = umulhi(x, m); d = 1 is the identity.
-struct FastDiv {
-    uint32_t m, l;
-};
-
-FastDiv make_fastdiv(uint32_t d)
-{
-    FastDiv f{0, 0};
-    if (d <= 1) return f;
-    while ((uint64_t(1) << f.l) < d) ++f.l;
-    f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << f.l) - d)) / d + 1);
-    return f;
-}
-
-__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f)
-{
-    if (f.l == 0) return x;
-    const uint32_t t = __umulhi(x, f.m);
-    return (t + ((x - t) >> 1)) >> (f.l - 1);
-}
-
 struct SortSrc {
     const int32_t* idx;
     int64_t is0, is1, is2;
@@ -85,7 +66,7 @@ __device__ __forceinline__ uint32_t sort_key(const SortSrc& s, uint32_t e, uint3
     int j = s.idx[int64_t(b) * s.is0 + int64_t(t) * s.is1 + int64_t(sl) * s.is2];
     j += (j >> 31) & int(s.T);
     j = min(max(j, 0), int(s.T) - 1);
-    val = t;
+    val = r;   // t * K + sl
     const bool masked = s.mask_pads && t + 1 < s.K && sl > t;
     return masked ? s.B * s.T : b * s.T + uint32_t(j);
 }
@@ -269,8 +250,19 @@ __device__ __forceinline__ int wrap_index(int j, int T)
     return min(max(j, 0), T - 1);
 }
 
+// Keep bits of slots slot_u (u < 2) of every lane group: lane sub < 2 of each group hashes its
+// group's slot_sub, and one ballot hands each group its two bits (groups are LPN >= 4 lanes).
+template <int LPN>
+__device__ __forceinline__ uint32_t drop_bits2(const DropoutParams& d, uint32_t row_key0,
+                                               uint32_t row_key1, uint32_t slot0, uint32_t slot1,
+                                               int sub, int grp)
+{
+    const bool mine = sub < 2 && drop_keep(d, sub == 0 ? row_key0 : row_key1, sub == 0 ? slot0 : slot1);
+    return uint32_t(__ballot(mine) >> (grp * LPN)) & 3u;
+}
+
 // Row pass: dq and delta for query rows t of one (b, h) pair.
-template <typename DT, int D>
+template <typename DT, int D, bool DROP>
 __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams p)
 {
     constexpr int LPN = D / 8;
@@ -312,6 +304,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
         if (!lane_on) { qlo = make_uint4(0, 0, 0, 0); qhi = qlo; glo = qlo; ghi = qlo; }
         const float lt2 = p.lse2[rbase + r];
         const int lim = (mask_flag && t < K - 1) ? t + 1 : K;   // slots >= lim carry no weight
+        const uint32_t rkey = DROP ? drop_row_key(p.drop, uint64_t(rbase + r)) : 0u;
         const int32_t* ip = ib + r * p.is[1];
         float A[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         float Bk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -326,10 +319,12 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
                 ld16<DT>(vb, uint32_t(j) * vrow + loff, vlo[u], vhi[u]);
             }
             float pu[2], pd[2];
+            const uint32_t kb2 = DROP ? drop_bits2<LPN>(p.drop, rkey, rkey, uint32_t(sl[0]), uint32_t(sl[1]), sub, grp) : 3u;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float d = group_sum<LPN>(dot8<DT>(qlo, qhi, klo[u], khi[u]));
-                const float dp = group_sum<LPN>(dot8<DT>(glo, ghi, vlo[u], vhi[u]));
+                float dp = group_sum<LPN>(dot8<DT>(glo, ghi, vlo[u], vhi[u]));
+                if (DROP) dp = (kb2 >> u) & 1u ? dp * p.drop.scale : 0.0f;
                 // v_exp_f32 directly: 2^(s - lse) <= 1; masked slots get no weight
                 pu[u] = sl[u] < lim ? __builtin_amdgcn_exp2f(d * sl2 - lt2) : 0.0f;
                 pd[u] = pu[u] * dp;
@@ -355,7 +350,7 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_rows(ReadoutBwdParams
 }
 
 // Key pass: dk and dv for key rows j of one (b, h) pair.
-template <typename DT, int D>
+template <typename DT, int D, bool DROP>
 __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams p)
 {
     constexpr int LPN = D / 8;
@@ -396,25 +391,37 @@ __global__ __launch_bounds__(64 * kWaves) void readout_bwd_keys(ReadoutBwdParams
         for (uint32_t e = e0; e < e1; e += 2 * NPS) {
             const uint32_t en[2] = {e + uint32_t(grp), e + uint32_t(NPS + grp)};
             int t[2];
+            uint32_t slot[2];
             uint4 qlo[2], qhi[2], glo[2], ghi[2];
             float2 st[2];   // (lse2, delta) of the entry's query row
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                t[u] = en[u] < e1 ? int(p.rows[en[u]]) : 0;
+                const uint32_t rv = en[u] < e1 ? p.rows[en[u]] : 0u;   // t * K + s
+                t[u] = int(fdiv(rv, p.divK));
+                slot[u] = rv - uint32_t(t[u]) * uint32_t(p.K);
                 ld16<DT>(qb, uint32_t(t[u]) * qrow + loff, qlo[u], qhi[u]);
                 ld16<DT>(gb, uint32_t(t[u]) * grow + loff, glo[u], ghi[u]);
                 st[u] = rs[t[u]];
             }
-            float pu[2], ds[2];
+            uint32_t kb2 = 3u;
+            if (DROP) {
+                const uint64_t rb0 = uint64_t(b * p.H + h) * uint64_t(p.T);
+                kb2 = drop_bits2<LPN>(p.drop, drop_row_key(p.drop, rb0 + uint64_t(t[0])),
+                                      drop_row_key(p.drop, rb0 + uint64_t(t[1])), slot[0], slot[1], sub, grp);
+            }
+            float pu[2], ds[2], pw[2];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float d = group_sum<LPN>(dot8<DT>(qlo[u], qhi[u], klo, khi));
-                const float dp = group_sum<LPN>(dot8<DT>(glo[u], ghi[u], vlo, vhi));
+                float dp = group_sum<LPN>(dot8<DT>(glo[u], ghi[u], vlo, vhi));
+                const float mc = DROP ? ((kb2 >> u) & 1u ? p.drop.scale : 0.0f) : 1.0f;
+                if (DROP) dp *= mc;
                 pu[u] = en[u] < e1 ? __builtin_amdgcn_exp2f(d * sl2 - st[u].x) : 0.0f;
                 ds[u] = pu[u] * (dp - st[u].y);
+                pw[u] = DROP ? pu[u] * mc : pu[u];   // the weight dout_t carries into dv
             }
             pv2<DT>(ak, ds[0], ds[1], qlo[0], qhi[0], qlo[1], qhi[1]);
-            pv2<DT>(av, pu[0], pu[1], glo[0], ghi[0], glo[1], ghi[1]);
+            pv2<DT>(av, pw[0], pw[1], glo[0], ghi[0], glo[1], ghi[1]);
         }
         float ok8[8], ov8[8];
 #pragma unroll
@@ -463,26 +470,32 @@ BwdLayout bwd_layout(int64_t B, int64_t H, int64_t T, int64_t K)
     return L;
 }
 
-template <typename DT>
+template <typename DT, bool DROP>
 hipError_t launch_passes(const ReadoutBwdParams& p, hipStream_t s)
 {
     const int64_t grid = 8 * (p.vpairs / 8) * p.wg_per_vpair;
     const dim3 g(static_cast<unsigned>(grid)), blk(64 * kWaves);
     // lane layout: the head dim padded to 32, 64, 128 or 256 (D / 8 lanes per neighbour)
     if (p.D <= 32) {
-        readout_bwd_rows<DT, 32><<<g, blk, 0, s>>>(p);
-        readout_bwd_keys<DT, 32><<<g, blk, 0, s>>>(p);
+        readout_bwd_rows<DT, 32, DROP><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 32, DROP><<<g, blk, 0, s>>>(p);
     } else if (p.D <= 64) {
-        readout_bwd_rows<DT, 64><<<g, blk, 0, s>>>(p);
-        readout_bwd_keys<DT, 64><<<g, blk, 0, s>>>(p);
+        readout_bwd_rows<DT, 64, DROP><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 64, DROP><<<g, blk, 0, s>>>(p);
     } else if (p.D <= 128) {
-        readout_bwd_rows<DT, 128><<<g, blk, 0, s>>>(p);
-        readout_bwd_keys<DT, 128><<<g, blk, 0, s>>>(p);
+        readout_bwd_rows<DT, 128, DROP><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 128, DROP><<<g, blk, 0, s>>>(p);
     } else {
-        readout_bwd_rows<DT, 256><<<g, blk, 0, s>>>(p);
-        readout_bwd_keys<DT, 256><<<g, blk, 0, s>>>(p);
+        readout_bwd_rows<DT, 256, DROP><<<g, blk, 0, s>>>(p);
+        readout_bwd_keys<DT, 256, DROP><<<g, blk, 0, s>>>(p);
     }
     return hipGetLastError();
+}
+
+template <typename DT>
+hipError_t launch_passes_t(const ReadoutBwdParams& p, hipStream_t s)
+{
+    return p.drop_on ? launch_passes<DT, true>(p, s) : launch_passes<DT, false>(p, s);
 }
 
 }  // namespace
@@ -530,9 +543,10 @@ hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, si
     p.row_stats = reinterpret_cast<float2*>(w + L.row_stats);
     p.off = off;
     p.rows = Z[1];
-    if (dtype == 2) return launch_passes<bf16_t>(p, s);
-    if (dtype == 1) return launch_passes<_Float16>(p, s);
-    return launch_passes<float>(p, s);
+    p.divK = make_fastdiv(uint32_t(p.K));
+    if (dtype == 2) return launch_passes_t<bf16_t>(p, s);
+    if (dtype == 1) return launch_passes_t<_Float16>(p, s);
+    return launch_passes_t<float>(p, s);
 }
 
 }  // namespace wf

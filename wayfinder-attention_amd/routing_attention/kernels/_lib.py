@@ -75,6 +75,12 @@ SIGNATURES = {
                                                  ctypes.c_float, ctypes.c_uint, _p, _i64p, _p, _p]),
     "wf_sparse_readout_bwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "wf_sparse_readout_bwd": (ctypes.c_int, [ctypes.POINTER(ReadoutBwdArgs), _p]),
+    "wf_sparse_readout_fwd_dropout": (ctypes.c_int, [_p, _p, _p, ctypes.c_int, _i64, _i64, _i64, _i64,
+                                                     _i64p, _i64p, _i64p, _p, _i64p, _i64,
+                                                     ctypes.c_float, ctypes.c_uint, ctypes.c_float,
+                                                     ctypes.c_uint64, _p, _i64p, _p, _p]),
+    "wf_sparse_readout_bwd_dropout": (ctypes.c_int, [ctypes.POINTER(ReadoutBwdArgs), ctypes.c_float,
+                                                     ctypes.c_uint64, _p]),
     "wf_address_project_fwd": (ctypes.c_int, [_p, ctypes.c_int, _i64, _i64, _i64, _i64p, _p, _p,
                                               _p, _p, _i64, _i64, ctypes.c_int, _p, _i64p, _p,
                                               _i64p, _p]),
@@ -87,7 +93,7 @@ SIGNATURES = {
                                        _p, _i64p, _i64, _p, ctypes.c_size_t, _p]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

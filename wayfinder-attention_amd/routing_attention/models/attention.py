@@ -9,7 +9,7 @@ With ``retrieval_config.use_fused_sparse`` each forward runs the fused HIP path
 reference's @torch.no_grad fused_sparse_attention. Its output is written directly in
 (B, T, H, D) memory, so the head merge before out_proj is a view, not a copy. The other
 branch retrieves with the HIP causal top-K and reads out with the HIP readout, forward and
-backward; only dropout in training takes the reference's gather formulation.
+backward, dropout in training included (inside the readout kernels).
 """
 
 from __future__ import annotations
@@ -47,34 +47,22 @@ def _use_fused_sparse_path(cfg: RetrievalConfig | None) -> bool:
     return bool(cfg and cfg.use_fused_sparse)
 
 
-def _gather_kv_heads(k: torch.Tensor, v: torch.Tensor,
-                     candidate_idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """k, v (B, H, T, D) at (B, T, K) shared indices -> (B, H, T, K, D) each (reference
-    attention.py:58-69). Only the dropout-in-training branch materialises these."""
-    B, H = k.shape[0], k.shape[1]
-    bi = torch.arange(B, device=k.device).view(B, 1, 1, 1)
-    hi = torch.arange(H, device=k.device).view(1, H, 1, 1)
-    ii = candidate_idx.long().unsqueeze(1)
-    return k[bi, hi, ii, :], v[bi, hi, ii, :]
-
-
 def _sparse_meat_forward(q, k, v, candidate_idx, scale: float, dropout: nn.Dropout,
                          cfg: RetrievalConfig | None) -> torch.Tensor:
     """Attention of each query over its K candidates, (B, H, T, D) (reference
     attention.py:35-55).
 
-    * dropout active (training with p > 0): the gather formulation with dropout on the
-      probabilities, as the reference's non-fused branch (torch ops on the GPU);
+    * dropout active (training with p > 0): ``sparse_readout`` with dropout on the
+      attention weights after the softmax, as the reference's non-fused branch, in the
+      HIP forward and backward (the keep mask is a hash of a seed drawn from torch's
+      generator, recomputed by the backward; nothing of size (B, H, T, K, D) is formed);
     * a gradient is needed: ``sparse_readout``, the HIP forward and backward (dq by a
       row pass, dk/dv over the transposed index lists, deterministic);
     * otherwise: the no-grad HIP readout ``sparse_meat_attention``.
     """
     del cfg
     if dropout.training and dropout.p > 0:
-        k_sel, v_sel = _gather_kv_heads(k, v, candidate_idx)
-        scores = (q.unsqueeze(3) * k_sel).sum(-1) * scale
-        attn = dropout(F.softmax(scores, dim=-1))
-        return (attn.unsqueeze(-1) * v_sel).sum(dim=3)
+        return sparse_readout(q, k, v, candidate_idx, scale, dropout_p=dropout.p)
     needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
     if needs_grad:
         return sparse_readout(q, k, v, candidate_idx, scale)
