@@ -122,6 +122,29 @@ def test_seeded_topk_repeatable_across_alphas(device, alpha):
 
 
 @pytest.mark.parametrize("mode", ["single", "split"])
+def test_burst_overflow_fused_paths(device, alpha, mode):
+    """Rows whose pools overflow in pass 0 through the fused forward: the single-pass kernel
+    must not read out a row before pass 1 has retrieved it again."""
+    _say(f"[seed] fused {mode}, burst keys")
+    alpha(None)
+    B, H, T, D, K, R = 1, 8, 8192, 64, 128, 32
+    qa, ka = addresses(B, T, R, seed=8192 + 5000, dtype=torch.float32)
+    mu = torch.ones(R) / R ** 0.5
+    qa = (qa + 0.5 * mu).to(torch.bfloat16)
+    ka[:, 5000:5600] = ka[:, 5000:5600] + 1.5 * mu
+    ka = ka.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(503)
+    q, k, v = (torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).transpose(1, 2) for _ in range(3))
+    cfg = SparseMeatConfig(fused_pass=mode)
+    out, idx = fused_sparse_attention(qa.to(device), ka.to(device), q.to(device), k.to(device),
+                                      v.to(device), K, D ** -0.5, meat_config=cfg)
+    torch.cuda.synchronize()
+    ref_idx = native.causal_topk(qa, ka, K)
+    assert torch.equal(idx.cpu(), ref_idx)
+    assert rel_err(out.float(), native.sparse_readout(q, k, v, ref_idx, D ** -0.5)) < 2e-2
+
+
+@pytest.mark.parametrize("mode", ["single", "split"])
 def test_seeded_fused_paths(device, alpha, mode):
     """Fused forward with seeds that fail often: the single-pass kernel reads each row's
     indices from LDS after the retrieval, so a failed row's pool must survive pass 0."""
