@@ -259,12 +259,12 @@ def bench_decoder(args):
             return model(ids)
 
     def dense_step():
+        # the same inference forward (fused residual-add + LayerNorm passes, head and loss),
+        # with attn_mask=None so every block's SDPA runs is_causal=True, its fastest form
         with torch.no_grad():
-            pos = torch.arange(c["T"], device=dev).unsqueeze(0)
-            x = dense.token_emb(ids) + dense.pos_emb(pos)
-            for blk in dense.blocks:
-                x = blk(x, attn_mask=None)      # causal SDPA (is_causal=True)
-            return dense.lm_head(dense.ln_f(x))
+            x = dense.token_emb(ids) + dense.pos_emb.weight[:c["T"]].unsqueeze(0)
+            logits = dense.lm_head(dense._blocks_fused_norms(x, None))
+            return dense._next_token_loss(logits, ids, ids != dense.pad_token_id)
 
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define WF_ABI_VERSION 4
+#define WF_ABI_VERSION 5
 
 typedef enum wf_status {
     WF_OK = 0,
@@ -227,6 +227,25 @@ int wf_address_project_fwd(const void* x, int dtype, int64_t B, int64_t T, int64
                            const void* wk, const void* bk, int64_t w_stride, int64_t R,
                            int normalize, void* out_q, const int64_t* oq_strides,
                            void* out_k, const int64_t* ok_strides, void* stream);
+
+/*
+ * Residual add + LayerNorm over the last dim, one pass.
+ * Replaces: in TransformerBlock.forward (routing_attention/models/transformer.py:50-73) and
+ *           the final norm (transformer.py:332), the pair `x = x + delta` followed by
+ *           nn.LayerNorm(x) (F.layer_norm, biased variance).
+ * x, delta    : (rows, n) of `dtype` at row strides x_stride / delta_stride (unit column
+ *               stride, 16-byte aligned rows); delta == NULL: LayerNorm of x alone.
+ * weight, bias: (n) of `dtype`, 16-byte aligned, or NULL (no affine scale / shift).
+ * sum_out     : x + delta, rounded to `dtype`, at sum_stride, or NULL (not written; also not
+ *               written when delta == NULL).
+ * y           : LayerNorm(x + delta) at y_stride: (s - mean) / sqrt(var + eps) * weight +
+ *               bias over each row of s = x + delta, computed in fp32 and rounded once.
+ * Limits: n % 8 == 0, n <= 1024. sum_out and y may not overlap x or delta.
+ */
+int wf_residual_layernorm_fwd(const void* x, const void* delta, int dtype, int64_t rows, int64_t n,
+                              int64_t x_stride, int64_t delta_stride, const void* weight,
+                              const void* bias, float eps, void* sum_out, int64_t sum_stride,
+                              void* y, int64_t y_stride, void* stream);
 
 /* Arguments of the fused forward, one struct so the entry point stays stable. */
 typedef struct wf_fused_args {

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.wf_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.wf_abi_version() == _lib.ABI_VERSION == 5
 
 
 def _i64(*v):
@@ -250,6 +250,34 @@ def test_address_contract_errors(lib, kw, code, msg):
 
 def test_address_empty_is_noop(lib):
     assert _addr(lib, B=0) == _lib.WF_OK
+
+
+def _ln(lib, **kw):
+    a = dict(x=FAKE, d=FAKE, dtype=2, rows=16, n=256, xs=256, ds=256, w=FAKE, b=FAKE, eps=1e-5,
+             s=FAKE, ss=256, y=FAKE, ys=256)
+    a.update(kw)
+    return lib.wf_residual_layernorm_fwd(a["x"], a["d"], a["dtype"], a["rows"], a["n"], a["xs"], a["ds"],
+                                         a["w"], a["b"], a["eps"], a["s"], a["ss"], a["y"], a["ys"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=7), _lib.WF_ERR_UNSUPPORTED, "dtype"),
+    (dict(n=260, xs=264, ds=264, ss=264, ys=264), _lib.WF_ERR_UNSUPPORTED, "multiple of 8"),
+    (dict(n=1032, xs=1032, ds=1032, ss=1032, ys=1032), _lib.WF_ERR_UNSUPPORTED, "at most 1024"),
+    (dict(rows=-1), _lib.WF_ERR_INVALID_ARGUMENT, "shape"),
+    (dict(eps=-1.0), _lib.WF_ERR_INVALID_ARGUMENT, "eps"),
+    (dict(y=None), _lib.WF_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(xs=128), _lib.WF_ERR_UNSUPPORTED, "strides"),
+    (dict(d=FAKE + 2), _lib.WF_ERR_UNSUPPORTED, "alignment"),
+    (dict(w=FAKE + 8), _lib.WF_ERR_UNSUPPORTED, "alignment"),
+])
+def test_layernorm_contract_errors(lib, kw, code, msg):
+    assert _ln(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_layernorm_empty_is_noop(lib):
+    assert _ln(lib, rows=0) == _lib.WF_OK
 
 
 def test_probe_gather_contract_errors(lib):

@@ -20,7 +20,8 @@ LIB = os.path.join(LIB_DIR, "libwayfinder_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 SOURCES = ["wf_abi.cpp", "wf_topk.hip", "wf_topk_bf16.hip", "wf_topk_f16.hip", "wf_topk_f32.hip",
-           "wf_fused.hip", "wf_readout.hip", "wf_readout_bwd.hip", "wf_address.hip", "wf_probe.hip"]
+           "wf_fused.hip", "wf_readout.hip", "wf_readout_bwd.hip", "wf_address.hip", "wf_layernorm.hip",
+           "wf_probe.hip"]
 
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",

@@ -591,6 +591,38 @@ int wf_address_project_fwd(const void* x, int dtype, int64_t B, int64_t T, int64
     return ok();
 }
 
+int wf_residual_layernorm_fwd(const void* x, const void* delta, int dtype, int64_t rows, int64_t n,
+                              int64_t x_stride, int64_t delta_stride, const void* weight,
+                              const void* bias, float eps, void* sum_out, int64_t sum_stride,
+                              void* y, int64_t y_stride, void* stream)
+{
+    if (!valid_dtype(dtype)) return fail(WF_ERR_UNSUPPORTED, "residual_layernorm: unsupported dtype code %d", dtype);
+    if (rows < 0 || n < 1)
+        return fail(WF_ERR_INVALID_ARGUMENT, "residual_layernorm: bad shape (rows=%lld, n=%lld)",
+                    (long long)rows, (long long)n);
+    if (n % 8 != 0 || n > 1024)
+        return fail(WF_ERR_UNSUPPORTED, "residual_layernorm: n=%lld (needs a multiple of 8, at most 1024)", (long long)n);
+    if (!(eps >= 0.0f)) return fail(WF_ERR_INVALID_ARGUMENT, "residual_layernorm: eps=%g", double(eps));
+    if (rows == 0) return ok();
+    if (!x || !y) return fail(WF_ERR_INVALID_ARGUMENT, "residual_layernorm: NULL x or y");
+    const int64_t es = int64_t(elem_size(dtype));
+    auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    auto rows_ok = [&](const void* p, int64_t stride) {
+        return p == nullptr || (a16(p) && stride >= n && (stride * es) % 16 == 0);
+    };
+    if (!rows_ok(x, x_stride) || !rows_ok(delta, delta_stride) || !rows_ok(sum_out, sum_stride) ||
+        !rows_ok(y, y_stride) || (weight && !a16(weight)) || (bias && !a16(bias)))
+        return fail(WF_ERR_UNSUPPORTED, "residual_layernorm: rows and parameters need 16-byte alignment "
+                                        "and strides of at least n");
+    wf::LayerNormParams p{};
+    p.x = x; p.delta = delta; p.weight = weight; p.bias = bias; p.sum_out = sum_out; p.y = y;
+    p.x_stride = x_stride; p.delta_stride = delta_stride; p.sum_stride = sum_stride; p.y_stride = y_stride;
+    p.rows = rows; p.n = n; p.eps = eps;
+    const hipError_t e = wf::launch_residual_layernorm(dtype, p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("residual_layernorm: kernel launch", e);
+    return ok();
+}
+
 size_t wf_probe_gather_sink_bytes(int64_t B, int64_t H, int64_t T)
 {
     if (B <= 0 || H <= 0 || T <= 0) return 0;

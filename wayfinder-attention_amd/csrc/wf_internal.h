@@ -279,6 +279,20 @@ hipError_t launch_sparse_readout(int dtype, bool vec, bool fast, const ReadoutPa
 size_t sparse_readout_bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t K);
 hipError_t launch_sparse_readout_bwd(int dtype, ReadoutBwdParams p, void* ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_address_project(int dtype, const AddressParams& p, hipStream_t s);
+
+// residual add + LayerNorm over the last dim (wf_layernorm.hip)
+struct LayerNormParams {
+    const void* x;           // (rows, n) at row stride x_stride, contiguous rows
+    const void* delta;       // same shape at delta_stride, or null (LayerNorm of x alone)
+    const void* weight;      // (n) or null
+    const void* bias;        // (n) or null
+    void* sum_out;           // x + delta (rows, n) at sum_stride, or null (not written)
+    void* y;                 // LayerNorm(x + delta) (rows, n) at y_stride
+    int64_t x_stride, delta_stride, sum_stride, y_stride;
+    int64_t rows, n;         // n % 8 == 0, n <= 1024
+    float eps;
+};
+hipError_t launch_residual_layernorm(int dtype, const LayerNormParams& p, hipStream_t s);
 // single-pass fused forward (wf_fused.hip): retrieval and all-heads readout in one kernel.
 // True if the shape and layout qualify (16-bit types, R = 32 on the aligned path,
 // 64 < k_eff <= 256, D / 8 lanes per head with H * D / 8 in {64, 128}).

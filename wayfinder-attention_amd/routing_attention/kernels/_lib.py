@@ -84,6 +84,8 @@ SIGNATURES = {
     "wf_address_project_fwd": (ctypes.c_int, [_p, ctypes.c_int, _i64, _i64, _i64, _i64p, _p, _p,
                                               _p, _p, _i64, _i64, ctypes.c_int, _p, _i64p, _p,
                                               _i64p, _p]),
+    "wf_residual_layernorm_fwd": (ctypes.c_int, [_p, _p, ctypes.c_int, _i64, _i64, _i64, _i64, _p, _p,
+                                                 ctypes.c_float, _p, _i64, _p, _i64, _p]),
     "wf_fused_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64]),
     "wf_fused_topk_sparse_fwd": (ctypes.c_int, [ctypes.POINTER(FusedArgs), _p]),
     "wf_fused_noalloc_scratch_limit": (ctypes.c_size_t, []),
@@ -93,7 +95,7 @@ SIGNATURES = {
                                        _p, _i64p, _i64, _p, ctypes.c_size_t, _p]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -19,6 +19,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from routing_attention.kernels import layernorm as _ln_kernel
 from routing_attention.models.attention import (
     DenseSDPAAttention,
     KeyVectorSparseAttention,
@@ -216,6 +217,12 @@ class TransformerLM(nn.Module):
         mask = attn_mask if attn_mask is not None else input_ids != self.pad_token_id
         x = self.dropout(self.token_emb(input_ids) + self.pos_emb.weight[:T].unsqueeze(0))
         caught = {"hidden_states": [], "attentions": [], "pre_attention_hidden": []}
+        plain = not (return_hidden_states or return_attentions or return_pre_attention_hidden
+                     or target_layer is not None or stop_after_layer is not None)
+        if plain and not self.training and not torch.is_grad_enabled() and x.is_cuda:
+            x = self._blocks_fused_norms(x, mask)
+            return self._head(x, input_ids, mask, labels, caught, return_hidden_states,
+                              return_attentions, return_pre_attention_hidden)
         for i, block in enumerate(self.blocks):
             watched = target_layer is None or i == target_layer
             if watched and return_pre_attention_hidden:
@@ -231,6 +238,36 @@ class TransformerLM(nn.Module):
             if watched and stop_after_layer is not None and i >= stop_after_layer:
                 break
         x = self.ln_f(x)
+        return self._head(x, input_ids, mask, labels, caught, return_hidden_states,
+                          return_attentions, return_pre_attention_hidden)
+
+    @staticmethod
+    def _add_norm(x: torch.Tensor, delta: torch.Tensor | None,
+                  ln: nn.LayerNorm) -> tuple[torch.Tensor, torch.Tensor]:
+        """(x + delta, ln(x + delta)) in one HIP pass where the kernel takes the shapes,
+        else with the PyTorch ops (same values up to the norm's fp32 summation order)."""
+        if _ln_kernel.supported(x, ln, delta):
+            return _ln_kernel.residual_layer_norm(x, delta, ln)
+        s = x if delta is None else x + delta
+        return s, ln(s)
+
+    def _blocks_fused_norms(self, x: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """Inference forward of the blocks and ln_f with every residual add fused into the
+        LayerNorm that follows it: per block attn(ln1 x), then x += a with ln2 in one pass,
+        ff(.), then x += f with the next block's ln1 (or ln_f) in one pass. Returns ln_f of
+        the last residual stream. Dropout is the identity here (eval mode)."""
+        blocks = list(self.blocks)
+        x, h = self._add_norm(x, None, blocks[0].ln1)
+        for i, block in enumerate(blocks):
+            a = block.attn(h, attn_mask=mask)
+            x, h = self._add_norm(x, a, block.ln2)
+            f = block.ff(h)
+            x, h = self._add_norm(x, f, blocks[i + 1].ln1 if i + 1 < len(blocks) else self.ln_f)
+        return h
+
+    def _head(self, x, input_ids, mask, labels, caught, return_hidden_states, return_attentions,
+              return_pre_attention_hidden) -> dict[str, torch.Tensor]:
+        """LM head, loss and the optional digit head over the final normalised stream x."""
         logits = self.lm_head(x)
         out: dict[str, torch.Tensor] = {"logits": logits,
                                         "loss": self._next_token_loss(logits, input_ids, mask)}
