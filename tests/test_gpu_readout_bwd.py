@@ -38,6 +38,10 @@ def _inputs(B, H, T, D, K, dtype, seed, idx_kind="topk", bthd=True):
     if idx_kind == "topk":
         qa, ka = addresses(B, T, 32, seed=seed + 1)
         idx = native.causal_topk(qa, ka, K)
+    elif idx_kind == "hub":   # skewed lists: 5/8 of every row's slots on six keys
+        idx = torch.randint(0, T, (B, T, K), generator=g).to(torch.int32)
+        nh = 5 * K // 8
+        idx[:, :, :nh] = torch.randint(0, 6, (B, T, nh), generator=g).to(torch.int32) * 7
     else:      # arbitrary indices: duplicates, negative (wrap) and out-of-range (clamp)
         idx = torch.randint(-T, T + 3, (B, T, K), generator=g).to(torch.int32)
         idx[:, :, 1] = idx[:, :, 0]
@@ -61,6 +65,10 @@ CASES = [
     (2, 3, 257, 64, 128, torch.bfloat16, "topk", False, True),
     (1, 4, 400, 64, 16, torch.float16, "random", False, True),
     (1, 2, 150, 128, 100, torch.bfloat16, "random", True, False),
+    # a few keys hold most entries: their lists are cut across the key pass's waves
+    (1, 2, 600, 64, 64, torch.float32, "hub", False, True),
+    (2, 2, 333, 128, 40, torch.float32, "hub", True, True),
+    (1, 3, 700, 64, 96, torch.bfloat16, "hub", False, True),
 ]
 
 
@@ -80,9 +88,10 @@ def test_readout_bwd_vs_autograd_oracle(device, case):
         assert err < tol, f"{name} rel err {err:.3e}"
 
 
-def test_readout_bwd_deterministic(device):
-    _say("[bwd] determinism")
-    q, k, v, dout, idx = _inputs(1, 4, 1024, 64, 128, torch.bfloat16, seed=11)
+@pytest.mark.parametrize("kind", ["topk", "hub"])
+def test_readout_bwd_deterministic(device, kind):
+    _say(f"[bwd] determinism ({kind} indices)")
+    q, k, v, dout, idx = _inputs(1, 4, 1024, 64, 128, torch.bfloat16, seed=11, idx_kind=kind)
     g1 = _hip_grads(q, k, v, dout, idx, 0.125, False, device)
     g2 = _hip_grads(q, k, v, dout, idx, 0.125, False, device)
     for a, b in zip(g1[1:], g2[1:]):
