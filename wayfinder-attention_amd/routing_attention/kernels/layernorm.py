@@ -25,10 +25,12 @@ def _rows_ok(t: torch.Tensor) -> bool:
 
 
 def supported(x: torch.Tensor, ln: nn.LayerNorm, delta: torch.Tensor | None = None) -> bool:
-    """Shapes and layouts the kernel takes (anything else stays on the PyTorch ops)."""
+    """Shapes and layouts the kernel takes, on a device where the library loads (anything
+    else stays on the PyTorch ops: this pass only fuses ops PyTorch already provides)."""
     n = x.shape[-1]
     params = [p for p in (ln.weight, ln.bias) if p is not None]
     return (x.is_cuda and x.dtype in _lib.WF_DTYPE and _rows_ok(x) and n % 8 == 0 and n <= MAX_WIDTH
+            and _lib.available()
             and tuple(ln.normalized_shape) == (n,)
             and (delta is None or (delta.shape == x.shape and delta.dtype == x.dtype and _rows_ok(delta)))
             and all(p.dtype == x.dtype and p.is_contiguous() and p.data_ptr() % 16 == 0 for p in params))
