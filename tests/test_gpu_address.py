@@ -30,6 +30,10 @@ CASES = [
     (3, 100, 520, 32, torch.float16, "symmetric", True, 8),
     (1, 129, 264, 20, torch.bfloat16, "asymmetric", False, 16),
     (2, 64, 1024, 32, torch.float32, "symmetric", True, 0),
+    # fewer tokens than one 16-token wave, spread over three batches (the MFMA kernel walks
+    # a wave's tokens across batch boundaries)
+    (3, 5, 64, 32, torch.bfloat16, "asymmetric", True, 0),
+    (1, 7, 128, 12, torch.float16, "asymmetric", True, 8),
 ]
 
 
