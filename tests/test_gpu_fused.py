@@ -56,6 +56,13 @@ def test_fused_config4_bf16(device):
     _fused_vs_oracle(device, 1, 8, 16384, 64, 32, 128, torch.bfloat16, 1004, 2e-2)
 
 
+def test_fused_fp16_long_rows(device):
+    """fp16 addresses and q/k/v, K not a power of two, prefixes long enough for the seeded
+    screen (T = 6000)."""
+    _say("[fused] fp16 B2 H4 T6000 D64 K100")
+    _fused_vs_oracle(device, 2, 4, 6000, 64, 32, 100, torch.float16, 1006, 2e-3)
+
+
 def test_fused_short_and_odd_shapes(device):
     _say("[fused] odd shapes")
     _fused_vs_oracle(device, 2, 3, 77, 32, 16, 128, torch.float16, 11, 2e-3)
