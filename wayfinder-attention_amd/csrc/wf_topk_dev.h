@@ -24,8 +24,9 @@
 //              (score desc, index asc) are radix-selected from the 64-bit keys.
 //  4. emit     The K winners are bitonic-sorted into canonical order and written with
 //              the reference's pad indices for rows that have fewer than K causal keys.
-//              For 64 < K <= 128 with at most K + 16 entries left after the final prune,
-//              the selection of step 3 and this sort are one network (emit_row_merge).
+//              For 64 < K <= 128 with at most 144 entries left after the final prune,
+//              and for 128 < K <= 256 with at most 320, the selection of step 3 and this
+//              sort are one network (emit_row_merge).
 //
 // Exactness: let E be the exact top-K of the keys seen so far and s_K its K-th score. The
 // pool always contains E: a pool holding K entries with MFMA score >= theta' has exact
@@ -726,39 +727,42 @@ __device__ uint64_t emit_row(const Entry* pool, int kept, int64_t row, int64_t T
     return kth;
 }
 
-// Exact selection fused into the sort, for K in (64, 128] and c <= 144 exactly scored
-// entries (after the final prune a K = 128 pool holds ~135): A = slots 0..127 is sorted
-// descending and B = slots 128..c-1 (at most 16, in lanes 14 and 15) descending; then
-// C[i] = max(A[i], B[127 - i]) holds the 128 largest of A and B as a bitonic sequence
-// (A falls, the reversed B rises), and one bitonic merge sorts it. This replaces the radix
-// select's histogram rounds with a 16-element sort, one exchange and seven merge steps.
+// Exact selection fused into the sort, for c <= KP2 + NB exactly scored entries (after the
+// final prune a K = 128 pool holds ~135, a K = 256 pool ~290): A = slots 0..KP2-1 is sorted
+// descending and B = slots KP2..c-1 (at most NB, in the last NB / EPL lanes) descending;
+// then C[i] = max(A[i], B[KP2-1 - i]) holds the KP2 largest of A and B as a bitonic
+// sequence (A falls, the reversed B rises), and one bitonic merge sorts it. This replaces
+// the radix select's histogram rounds with an NB-element sort, one exchange and log2(KP2)
+// merge steps. B[KP2-1 - i] for element i = EPL u + m of a B lane is register EPL-1 - m of
+// lane u ^ LXB (KP2 = 128, NB = 16: lanes 14, 15 and LXB = 1; KP2 = 256, NB = 64: lanes
+// 12..15 and LXB = 3); the other lanes pair with lanes whose B keys are 0.
 // Returns the row's k_eff-th key in canonical order (0 if fewer than k_eff were kept); the
 // LDS copy goes to lidx only if that key's score reaches lidx_min.
-template <int POOL>
+template <int KP2, int NB, int LXB, int POOL>
 __device__ uint64_t emit_row_merge(const Entry* pool, int c, int64_t row, int64_t T, int64_t k_eff,
                                    int32_t* out_idx, float* out_scores, int32_t* lidx,
                                    float lidx_min, int u)
 {
-    constexpr int KP2 = 128, EPL = 8, NB = 16;
+    constexpr int EPL = KP2 / 16;
     static_assert(POOL >= KP2 + NB, "pool too small");
+    static_assert((KP2 == 128 && NB == 16 && LXB == 1) || (KP2 == 256 && NB == 64 && LXB == 3),
+                  "lane pairing of the reversed B");
     uint64_t key[EPL], bkey[EPL];
 #pragma unroll
     for (int m = 0; m < EPL; ++m) {
         const int i = u * EPL + m;   // reads are unconditional (slots < KP2 + NB <= POOL), masked
         const uint2 ea = reinterpret_cast<const uint2*>(pool)[i];
         key[m] = i < c ? make_key(__uint_as_float(ea.x), ea.y) : 0ull;
-        const int jb = i - (KP2 - NB);   // B entry of element i of lanes 14 and 15
+        const int jb = i - (KP2 - NB);   // B entry of element i of the B lanes
         const int sb = KP2 + (jb < 0 ? 0 : jb);
         const uint2 eb = reinterpret_cast<const uint2*>(pool)[sb];
         bkey[m] = jb >= 0 && sb < c ? make_key(__uint_as_float(eb.x), eb.y) : 0ull;
     }
     bitonic_sort<EPL, KP2>(key, u);
-    bitonic_sort<EPL, NB>(bkey, u);   // lane 14: B[0..7], lane 15: B[8..15]; other lanes 0
-    // B[127 - i] for element i = 8u + m of lanes 14 and 15 is element 7 - m of the other lane
-    // of the pair; the other lanes pair with lanes whose B keys are 0
+    bitonic_sort<EPL, NB>(bkey, u);   // the B lanes hold B sorted; the other lanes hold 0
 #pragma unroll
     for (int m = 0; m < EPL; ++m) {
-        const uint64_t o = lane_xor16_u64(bkey[EPL - 1 - m], 1, u);
+        const uint64_t o = lane_xor16_u64(bkey[EPL - 1 - m], LXB, u);
         key[m] = o > key[m] ? o : key[m];
     }
     bitonic_merge<EPL, KP2>(key, u);
@@ -1206,13 +1210,15 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
             const float lidx_min = checked ? sd + sm.eps[rr] : -__builtin_inff();
             bool done = false;
             uint64_t kth = 0;   // the row's K-th best key (exact score), 0 if it kept fewer
-            if constexpr (KP2 == 128) {
-                if (cw2 <= KP2 + 16) {   // wave-uniform: selection fused into the sort
+            if constexpr (KP2 == 128 || KP2 == 256) {
+                constexpr int NB = KP2 == 128 ? 16 : 64;
+                if (cw2 <= KP2 + NB) {   // wave-uniform: selection fused into the sort
                     rescore_row<DT, VEC, RP>(sm.pool[rr], c, sm.q[rr], kb, p.kst, p.ksr, R, u);
 #ifdef WF_TOPK_TIMING
                     tmB = wall_clock64();
 #endif
-                    kth = emit_row_merge<POOL>(sm.pool[rr], c, r0 + rr, T, p.k_eff, oidx, oscr, lidx, lidx_min, u);
+                    kth = emit_row_merge<KP2, NB, KP2 == 128 ? 1 : 3, POOL>(sm.pool[rr], c, r0 + rr, T, p.k_eff,
+                                                                        oidx, oscr, lidx, lidx_min, u);
                     done = true;
                 }
             }
