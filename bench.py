@@ -202,6 +202,9 @@ def run_leg(args, dev, K, scale, readout_bytes):
         ms = time_loop(fn, args.steps, args.warmup)
         print(json.dumps({"leg": "topk", "ms": round(ms, 4)}), flush=True)
         return
+    if args.leg == "topk-phases":
+        print(json.dumps(topk_phases(dev, K)), flush=True)
+        return
     idx = causal_topk(dev["qa"], dev["ka"], K)
     if args.leg == "backward":
         from routing_attention.kernels.sparse_autograd import readout_bwd, readout_fwd_lse
@@ -230,6 +233,42 @@ def run_leg(args, dev, K, scale, readout_bytes):
     ms = time_loop(fn, args.steps, args.warmup)
     print(json.dumps({"leg": "readout", "ms": round(ms, 4),
                       "algorithmic_gbs": round(readout_bytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
+def topk_phases(dev, K):
+    """Per-workgroup phase times of one retrieval launch, from the measurement build's
+    timers (8 uint64 per workgroup in place of the scores; layout at WF_TOPK_TIMING in
+    csrc/wf_topk_dev.h). Means over the launch's row blocks, in microseconds: seed, screen
+    (after the seed, in-loop prunes included), final prune, exact rescoring + selection,
+    sort + write; slot_busy = summed block time / (resident workgroups x span)."""
+    import numpy as np
+    from routing_attention.kernels.causal_topk import _run_topk
+
+    qa, ka = dev["qa"], dev["ka"]
+    for _ in range(3):   # the last launch is read; the others warm up
+        _, sc = _run_topk(qa, ka, K, True)
+    torch.cuda.synchronize()
+    B, T, R = qa.shape
+    nblk = B * ((T + 15) // 16)
+    tm = sc.reshape(-1).view(torch.int64)[: 8 * nblk].cpu().numpy().reshape(nblk, 8)
+    t0, t1, t2, pk, ta, tb, ts, cc = (tm[:, i] for i in range(8))
+    if not ((t0 > 0).all() and (t1 >= t0).all() and (t2 >= t1).all() and (ts >= t0).all()):
+        raise RuntimeError("the retrieval wrote no phase timers: not the measurement build")
+    us = 0.01   # 100 MHz ticks
+    span = float(t2.max() - t0.min()) * us
+    summed = float((t2 - t0).sum()) * us
+    wide = (R + 31) // 32 > 2 or min(K, T) > 256
+    slots = torch.cuda.get_device_properties(qa.device).multi_processor_count * (1 if wide else 2)
+    m = lambda x: round(float(np.mean(x)) * us, 2)  # noqa: E731
+    return {"leg": "topk-phases", "blocks": int(nblk), "span_us": round(span, 1),
+            "slots": int(slots), "slot_busy": round(summed / (slots * span), 3),
+            "seed_us": m(ts - t0), "screen_us": m(t1 - ts), "inloop_prune_us": m(pk >> 32),
+            "inloop_prunes": round(float(np.mean((pk >> 16) & 0xffff)), 2),
+            "final_prune_us": m(ta - t1), "exact_us": m(tb - ta), "emit_us": m(t2 - tb),
+            "finish_us": m(t2 - t1), "pool_before_final_prune": round(float(np.mean(cc & 0xffffff)), 1),
+            "pool_after_final_prune": round(float(np.mean(cc >> 32)), 1),
+            "second_pass_blocks": int((((cc >> 24) & 0xf) > 1).sum()),
+            "overflowed_rows": int(((cc >> 28) & 0xf).sum())}
 
 
 C2 = dict(vocab=128, d_model=256, n_layers=4, n_heads=4, d_ff=1024, T=2048, B=8, K=128)
@@ -323,10 +362,13 @@ def main():
     ap.add_argument("--cpu-runs", type=int, default=3, help="timed runs of the CPU baseline")
     ap.add_argument("--fused-pass", default="auto", choices=["auto", "split", "single"],
                     help="fused forward as two kernels (split), one kernel (single) or the library's choice")
-    ap.add_argument("--leg", default="all", choices=["all", "fused", "topk", "readout", "backward", "copy", "gather"],
+    ap.add_argument("--leg", default="all",
+                    choices=["all", "fused", "topk", "topk-phases", "readout", "backward", "copy", "gather"],
                     help="profiling aid: run only one kernel (or a 256 MiB device copy used to "
                          "calibrate the FETCH_SIZE / WRITE_SIZE counters, or the readout against "
-                         "its gather-path probe) and print its timing")
+                         "its gather-path probe) and print its timing; topk-phases reads the "
+                         "retrieval's per-workgroup phase timers from the measurement build "
+                         "(python wayfinder-attention_amd/build.py --timing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this path has no multi-GPU code "
@@ -336,6 +378,11 @@ def main():
     if args.config == "c2":
         bench_decoder(args)
         return
+    if args.leg == "topk-phases":   # before the library loads: the measurement build
+        lib = os.path.join(ROOT, "wayfinder-attention_amd", "lib", "libwayfinder_hip_timing.so")
+        if not os.path.exists(lib):
+            sys.exit(f"{lib} is missing: build it with python wayfinder-attention_amd/build.py --timing")
+        os.environ["WAYFINDER_HIP_LIB"] = lib
 
     from routing_attention.kernels import causal_topk, fused_sparse_attention, sparse_meat_attention
 

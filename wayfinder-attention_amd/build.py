@@ -56,6 +56,44 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+# Measurement build: the retrieval's translation units compiled with WF_TOPK_TIMING, linked
+# with the product's other objects into lib/libwayfinder_hip_timing.so. Its retrieval records
+# per-workgroup phase timestamps in place of the scores (read by bench.py --leg topk-phases);
+# indices are unchanged. Not loaded by anything else.
+TIMING_LIB = os.path.join(LIB_DIR, "libwayfinder_hip_timing.so")
+TIMING_SOURCES = ["wf_topk.hip", "wf_topk_bf16.hip", "wf_topk_f16.hip", "wf_topk_f32.hip"]
+
+
+def build_timing(verbose: bool = False) -> str:
+    build(verbose)
+    tdir = os.path.join(OBJ, "timing")
+    os.makedirs(tdir, exist_ok=True)
+
+    def comp(src: str) -> str:
+        obj = os.path.join(tdir, os.path.splitext(src)[0] + ".o")
+        cmd = [HIPCC, *COMMON, "-DWF_TOPK_TIMING", "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src} (timing):\n{r.stdout}\n{r.stderr}")
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=len(TIMING_SOURCES)) as ex:
+        tobjs = list(ex.map(comp, TIMING_SOURCES))
+    rest = [os.path.join(OBJ, os.path.splitext(s)[0] + ".o") for s in SOURCES if s not in TIMING_SOURCES]
+    tmp = TIMING_LIB + ".tmp"
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *tobjs, *rest, "-o", tmp],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc link failed (timing):\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, TIMING_LIB)
+    if verbose:
+        print(f"built {TIMING_LIB}")
+    return TIMING_LIB
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--timing" in sys.argv[1:]:
+        build_timing(verbose=True)
+    else:
+        build(verbose=True)
     sys.exit(0)

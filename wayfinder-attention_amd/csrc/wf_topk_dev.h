@@ -944,6 +944,13 @@ __device__ __forceinline__ void causal_topk_body(const TopkParams& p, const Tail
     __syncthreads();
 
 #ifdef WF_TOPK_TIMING
+    // Measurement build only (build.py --timing; bench.py --leg topk-phases reads it): the
+    // retrieval runs unchanged, but out_scores carries 8 uint64 per workgroup instead of
+    // scores (index = the workgroup's dispatch position), in wall-clock ticks (100 MHz):
+    // [0] after set-up, [1] end of the screen, [2] end of the block, [3] row block |
+    // in-loop prunes << 16 | their ticks << 32, [4] after the final prune, [5] after exact
+    // rescoring and selection, [6] after the seed, [7] pool count before the final prune |
+    // passes << 24 | overflowed rows << 28 | count after it << 32.
     uint64_t tm0 = wall_clock64();
     uint64_t tcomp = 0, ncomp = 0;
     uint64_t tm1 = 0, tmA = 0, tmB = 0;
