@@ -12,6 +12,7 @@ stretched pool checks and pruning, each bit-exact (indices and scores) against t
   the normal addresses);
 * planted -- sharp single winners;
 * mixed shapes, batches, K and input types with the default seed settings.
+* 128 < K <= 256 on random shapes, where the final selection runs inside the sort.
 """
 
 from __future__ import annotations
@@ -86,6 +87,30 @@ def test_topk_patterns_match_oracle(device, kind, B, T, R, K, dtype):
     bad = (idx.cpu() != ri).any(-1).nonzero()
     assert bad.numel() == 0, f"index mismatch at (b,t) {bad[:6].tolist()}"
     assert torch.equal(sc.cpu(), rs)
+
+
+def test_topk_k256_select_in_sort(device):
+    """Twelve shapes with 128 < K <= 256 and prefixes long enough that the final pools hold
+    more than K entries, so the selection runs inside the sort (up to 64 entries past K in
+    the last four lanes of a row) or, for fuller pools, through the radix select: B 1-2,
+    T 600-9000, R in {32, 64}, every input type, normal or Student-t addresses."""
+    g = torch.Generator().manual_seed(2027)
+    dtypes = [torch.bfloat16, torch.float16, torch.float32]
+    for i in range(12):
+        B = int(torch.randint(1, 3, (1,), generator=g))
+        T = int(torch.randint(600, 9001, (1,), generator=g))
+        R = [32, 64][int(torch.randint(0, 2, (1,), generator=g))]
+        K = int(torch.randint(129, 257, (1,), generator=g))
+        dtype = dtypes[i % 3]
+        dist = "student_t" if i % 2 else "normal"
+        _say(f"[patterns] K256 {i}: B{B} T{T} R{R} K{K} {dtype} {dist}")
+        qa, ka = addresses(B, T, R, seed=300 + i, dtype=dtype, dist=dist)
+        idx, sc = causal_topk_with_scores(qa.to(device), ka.to(device), K)
+        torch.cuda.synchronize()
+        ri, rs = native.causal_topk(qa, ka, K, return_scores=True)
+        bad = (idx.cpu() != ri).any(-1).nonzero()
+        assert bad.numel() == 0, f"case {i}: index mismatch at (b,t) {bad[:6].tolist()}"
+        assert torch.equal(sc.cpu(), rs), f"case {i}: scores differ"
 
 
 def test_topk_random_shapes(device):
